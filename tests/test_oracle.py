@@ -1,0 +1,379 @@
+"""Pins the CPU oracle (oracle/e5ma_oracle.c) before anything is checked against it.
+
+Each oracle function is held to something it does not compute itself:
+  * the reference's own exact MAC model (golden digests + vectors in tests/golden/, and the model
+    itself when oracle/_ref/libref.so was built from the reference sources);
+  * an exact rational (Fraction) model written here;
+  * independent codecs (torch's float8 / bfloat16 casts, numpy's float16 cast, a midpoint search);
+  * closed forms (single-product GEMMs, Adam with unit moments) and the reference's KATs.
+Negative controls plant a mistake in an oracle-side value and check the checker rejects it.
+"""
+import hashlib
+import json
+import os
+from fractions import Fraction as Fr
+
+import numpy as np
+import pytest
+import torch
+
+GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+PAIRINGS = [(1, 1), (1, 0), (0, 1), (0, 0)]
+
+
+@pytest.fixture(scope="module")
+def golden():
+    with open(os.path.join(GOLD, "lane_golden.json")) as f:
+        meta = json.load(f)
+    return meta, np.load(os.path.join(GOLD, "lane_golden.npz"))
+
+
+# ---- the exact MAC model -------------------------------------------------------------------------
+@pytest.mark.parametrize("fa,fb", PAIRINGS)
+def test_lane_full_sweep_matches_reference_digest(orc, golden, fa, fb):
+    meta, _ = golden
+    out = orc.lane_sweep(np.array(meta["corpus"], np.uint16), fa, fb)
+    assert hashlib.sha256(out.astype("<u2").tobytes()).hexdigest() == meta["sha256"][f"{fa}{fb}"]
+
+
+@pytest.mark.parametrize("fa,fb", PAIRINGS)
+def test_lane_matches_reference_vectors(orc, golden, fa, fb):
+    _, z = golden
+    t = f"{fa}{fb}"
+    got = orc.lane(z[f"a_{t}"], z[f"b_{t}"], z[f"acc_{t}"], fa, fb)
+    np.testing.assert_array_equal(got, z[f"out_{t}"])
+
+
+@pytest.mark.parametrize("fa,fb", PAIRINGS)
+def test_lane_against_reference_library(orc, fa, fb):
+    ref = orc.ref_library()
+    if ref is None:
+        pytest.skip("oracle/_ref/libref.so not built (reference sources absent)")
+    import ctypes
+    accs = np.arange(0, 0x10000, 97, dtype=np.uint16)  # 676 accumulators x 65,536 pairs
+    first = ctypes.c_uint32(0)
+    bad = orc.lib().orc_lane_compare(ctypes.cast(ref.ref_lane, ctypes.c_void_p), orc._p(accs), accs.size, fa, fb,
+                                     ctypes.byref(first))
+    assert bad == 0, hex(first.value)
+
+
+def _fp8_frac(code, fmt):
+    s, c = code >> 7, code & 0x7F
+    if fmt == 1:
+        e, f = c >> 2, c & 3
+        if e == 31:
+            return None
+        v = Fr(f, 4) * Fr(2) ** -14 if e == 0 else (1 + Fr(f, 4)) * Fr(2) ** (e - 15)
+    else:
+        e, f = c >> 3, c & 7
+        if c == 0x7F:
+            return None
+        v = Fr(f, 8) * Fr(2) ** -6 if e == 0 else (1 + Fr(f, 8)) * Fr(2) ** (e - 7)
+    return -v if s else v
+
+
+def _bf16_frac(h):
+    e, f = (h >> 7) & 0xFF, h & 0x7F
+    v = Fr(f, 128) * Fr(2) ** -126 if e == 0 else (1 + Fr(f, 128)) * Fr(2) ** (e - 127)
+    return -v if h >> 15 else v
+
+
+def _rn_bf16(x):
+    """Round a Fraction to BF16 bits by exact comparison with the neighbours (ties to even)."""
+    if x == 0:
+        return 0
+    s = 0x8000 if x < 0 else 0
+    a = -x if x < 0 else x
+    lo, hi = 0, 0x7F80  # bits of finite non-negative BF16 values are ordered like the values
+    while hi - lo > 1:
+        mid = (lo + hi) // 2
+        if _bf16_frac(mid) <= a:
+            lo = mid
+        else:
+            hi = mid
+    vl = _bf16_frac(lo)
+    vh = _bf16_frac(hi) if hi < 0x7F80 else Fr(2) ** 128  # Inf stands where 2^128 would be
+    if a == vl:
+        return s | lo
+    mid = (vl + vh) / 2
+    pick = lo if a < mid else hi if a > mid else (lo if lo % 2 == 0 else hi)
+    return s | pick
+
+
+@pytest.mark.parametrize("fa,fb", PAIRINGS)
+def test_lane_against_fraction_model(orc, fa, fb):
+    rng = np.random.default_rng(7 + fa * 2 + fb)
+    a = rng.integers(0, 256, 3000).astype(np.uint8)
+    b = rng.integers(0, 256, 3000).astype(np.uint8)
+    acc = rng.integers(0, 0x7F80, 3000).astype(np.uint16) | (rng.integers(0, 2, 3000).astype(np.uint16) << 15)
+    got = orc.lane(a, b, acc, fa, fb)
+    for x, y, c, g in zip(a.tolist(), b.tolist(), acc.tolist(), got.tolist()):
+        va, vb = _fp8_frac(x, fa), _fp8_frac(y, fb)
+        if va is None or vb is None:
+            assert g == 0x7FC0
+            continue
+        total = _bf16_frac(c) + va * vb
+        if total == 0:
+            both_neg_zero = va * vb == 0 and _bf16_frac(c) == 0 and (c >> 15) and ((x ^ y) >> 7)
+            assert g == (0x8000 if both_neg_zero else 0)
+        else:
+            assert g == _rn_bf16(total), (hex(x), hex(y), hex(c))
+
+
+# ---- codecs ----------------------------------------------------------------------------------------
+@pytest.mark.parametrize("fmt,tdt", [(4, torch.float8_e5m2), (0, torch.float8_e4m3fn)])
+def test_fp8_decode_all_codes_vs_torch(orc, fmt, tdt):
+    codes = np.arange(256, dtype=np.uint8)
+    got = orc.decode(fmt, codes)
+    ref = torch.from_numpy(codes).view(tdt).float().numpy()
+    assert np.array_equal(np.isnan(got), np.isnan(ref))
+    ok = ~np.isnan(ref)
+    assert np.array_equal(got[ok].view(np.uint32), ref[ok].view(np.uint32))  # bit equality: signed zeros too
+
+
+def test_fp8_operand_decode_reads_special_codes_as_finite(orc):
+    # reference src/e5m2effma.cuh:59-68 (E5M2 exponent-31 codes) and :43-52 (E4M3 0x7F -> 480)
+    L = orc.lib()
+    assert [L.orc_e5m2_operand(c) for c in (0x7C, 0x7D, 0x7E, 0x7F)] == [65536.0, 81920.0, 98304.0, 114688.0]
+    assert L.orc_e4m3_operand(0x7F) == 480.0 and L.orc_e4m3_operand(0xFF) == -480.0
+    for c in range(256):
+        if (c & 0x7C) != 0x7C:
+            assert L.orc_e5m2_operand(c) == L.orc_e5m2_value(c) or (c & 0x7F) == 0
+
+
+@pytest.mark.parametrize("fmt", [4, 0])
+def test_fp8_encoder_vs_midpoint_search(orc, fmt):
+    import ctypes
+    first = ctypes.c_uint32(0)
+    L = orc.lib()
+    # the whole 2^32 space at a prime stride, then every pattern of the FP8 range at a finer stride
+    assert L.orc_encode_selfcheck(fmt, 0, 1 << 32, 65521, ctypes.byref(first)) == 0, hex(first.value)
+    lo, hi = (0x37000000, 0x47800000) if fmt == 4 else (0x3B000000, 0x44000000)
+    for sign in (0, 0x80000000):
+        assert L.orc_encode_selfcheck(fmt, sign + lo, sign + hi, 509, ctypes.byref(first)) == 0, hex(first.value)
+
+
+@pytest.mark.parametrize("fmt,tdt,top", [(4, torch.float8_e5m2, 57344.0), (0, torch.float8_e4m3fn, 448.0)])
+def test_fp8_encoder_vs_torch_in_range(orc, fmt, tdt, top):
+    rng = np.random.default_rng(11)
+    x = np.concatenate([rng.standard_normal(200000).astype(np.float32) * s for s in (1e-6, 1e-3, 1.0, 100.0)])
+    x = np.concatenate([x, orc.decode(fmt, np.arange(256, dtype=np.uint8))])  # exact codes and midpoints
+    vals = orc.decode(fmt, np.arange(0, 0x7F, dtype=np.uint8)).astype(np.float64)
+    x = np.concatenate([x, ((vals[:-1] + vals[1:]) / 2).astype(np.float32)])
+    x = x[np.isfinite(x) & (np.abs(x) < top)]
+    got = orc.encode(fmt, x)
+    ref = torch.from_numpy(x).to(tdt).view(torch.uint8).numpy()
+    assert np.array_equal(got, ref)
+
+
+def test_fp8_encoder_kat(orc):
+    # reference binds/python/tests/test_e5m2effma.py:122-125 (saturation as cvt.rn.satfinite)
+    codes, amax = orc.cast(3, 4, np.array([1.0, np.inf, -1e6, 3.0], np.float32), 4)
+    assert codes.tolist() == [0x3C, 0x7B, 0xFB, 0x42] and amax == np.inf
+    nan = np.array([np.nan, -np.nan], np.float32)
+    assert orc.encode(4, nan).tolist() == [0x7F, 0x7F] and orc.encode(0, nan).tolist() == [0x7F, 0x7F]
+    assert orc.encode(0, np.array([448.0, 464.0, 1e9, -np.inf], np.float32)).tolist() == [0x7E, 0x7E, 0x7E, 0xFE]
+
+
+def test_bf16_rne_vs_torch(orc):
+    rng = np.random.default_rng(3)
+    u = rng.integers(0, 1 << 32, 2_000_000, dtype=np.uint64).astype(np.uint32)
+    u = np.concatenate([u, np.arange(0x7F7F0000, 0x7F800000, 7, dtype=np.uint32),
+                        (np.arange(0, 0x20000, dtype=np.uint32) | 0x3F800000)])  # overflow edge, all ties
+    x = u.view(np.float32)
+    got = orc.encode(1, x)
+    isnan = np.isnan(x)
+    assert (got[isnan] == 0x7FC0).all()
+    ref = torch.from_numpy(x[~isnan]).to(torch.bfloat16).view(torch.uint16).numpy()
+    assert np.array_equal(got[~isnan], ref)
+
+
+def test_f16_rne_vs_numpy(orc):
+    rng = np.random.default_rng(5)
+    u = rng.integers(0, 1 << 32, 2_000_000, dtype=np.uint64).astype(np.uint32)
+    u = np.concatenate([u, np.arange(0x33000000, 0x47800000, 613, dtype=np.uint32)])  # the whole f16 range
+    x = u.view(np.float32)
+    got = orc.encode(2, x)
+    isnan = np.isnan(x)
+    assert np.isnan(orc.decode(2, got[isnan])).all()
+    with np.errstate(over="ignore"):
+        ref = x[~isnan].astype(np.float16).view(np.uint16)
+    assert np.array_equal(got[~isnan], ref)
+    h = np.arange(0x10000, dtype=np.uint16)
+    dec = orc.decode(2, h)
+    ref = h.view(np.float16).astype(np.float32)
+    assert np.array_equal(np.isnan(dec), np.isnan(ref)) and np.array_equal(dec[~np.isnan(ref)], ref[~np.isnan(ref)])
+
+
+def test_cast_semantics(orc):
+    """load * sinv, NaN-ignoring amax committed only when positive, store with qscale
+    (reference src/e5m2effma.cu:53-63, src/e5m2effma.cuh:190-195)."""
+    codes = np.arange(256, dtype=np.uint8)
+    out, amax = orc.cast(4, 3, codes, 256, sinv=0.5)
+    ref = torch.from_numpy(codes).view(torch.float8_e5m2).float().numpy() * np.float32(0.5)
+    assert np.array_equal(np.isnan(out), np.isnan(ref)) and np.array_equal(out[~np.isnan(ref)], ref[~np.isnan(ref)])
+    assert amax == np.inf  # Inf enters amax, NaN does not
+    out, amax = orc.cast(3, 1, np.array([np.nan, -2.0, 1.0], np.float32), 3)
+    assert amax == 2.0 and out.tolist() == [0x7FC0, 0xC000, 0x3F80]
+    _, amax = orc.cast(3, 1, np.zeros(4, np.float32), 4, amax_in=-1.0)
+    assert amax == -1.0  # a zero partial maximum is not committed
+    _, amax = orc.cast(3, 1, np.array([0.5], np.float32), 1, amax_in=-1.0)
+    assert amax == 0.5
+
+
+# ---- GEMM semantics ----------------------------------------------------------------------------------
+def _rand_fp8(rng, n, fmt):
+    c = rng.integers(0, 256, n).astype(np.uint8)
+    bad = (c & 0x7C) == 0x7C if fmt == 4 else (c & 0x7F) == 0x7F
+    c[bad] ^= 4 if fmt == 4 else 1  # finite neighbours, as the reference fixtures draw them
+    return c
+
+
+def test_gemm_single_product_is_exact(orc):
+    """With one non-zero k per output the FP32 sum is exact: D = convert((alpha*sa)*sb * a*b)."""
+    rng = np.random.default_rng(1)
+    m, n, k = 8, 8, 16
+    A = np.zeros(k * m, np.uint8)
+    B = np.zeros(k * n, np.uint8)
+    a = _rand_fp8(rng, m, 4)
+    b = _rand_fp8(rng, n, 0)
+    A[np.arange(m) * k + 3] = a  # transa = T: A[kk + i*lda]
+    B[np.arange(n) * k + 3] = b  # transb = N: B[kk + j*ldb]
+    g = orc.Gemm(1, 0, m, n, k, 1.0, 4, A, k, 0, B, k, sa=[0.5], sb=[2.0], ddt=3)
+    g.chain()
+    va, vb = orc.decode(4, a).astype(np.float64), orc.decode(0, b).astype(np.float64)
+    np.testing.assert_array_equal(g.D.reshape(n, m), np.outer(vb, va).astype(np.float32))
+
+
+def _mk_case(orc, rng, ta, tb, at, bt, m, n, k):
+    lda = (k if ta else m) + 16
+    ldb = (k if not tb else n) + 16
+    na, nb = lda * (m if ta else k), ldb * (n if not tb else k)
+    def fill(dt, size):
+        if dt in (4, 0):
+            return _rand_fp8(rng, size, dt)
+        x = rng.uniform(-2, 2, size).astype(np.float32)
+        return orc.encode(dt, x) if dt == 1 else x
+    return fill(at, na), lda, fill(bt, nb), ldb
+
+
+@pytest.mark.parametrize("ta,tb", [(1, 0), (0, 0), (0, 1), (1, 1)])
+@pytest.mark.parametrize("at,bt", [(4, 4), (4, 0), (0, 1), (3, 4), (1, 3)])
+def test_gemm_chain_within_exact_bound(orc, ta, tb, at, bt):
+    rng = np.random.default_rng(ta * 2 + tb)
+    m, n, k = 37, 29, 48
+    A, lda, B, ldb = _mk_case(orc, rng, ta, tb, at, bt, m, n, k)
+    bias = rng.uniform(-8, 8, m).astype(np.float32)
+    C = rng.uniform(-4, 4, (m + 1) * n).astype(np.float32)
+    g = orc.Gemm(ta, tb, m, n, k, 1.25, at, A, lda, bt, B, ldb, sa=[0.37], sb=[1.9], beta=0.5, cdt=3, C=C, ldc=m + 1,
+                 ddt=3, bias=bias, biasdt=3)
+    amax = g.chain()
+    iis, jjs = np.meshgrid(np.arange(m), np.arange(n), indexing="ij")
+    # the FFMA chain's own error is far inside the bound the kernels are held to
+    bad, first, alo, ahi = g.check(g.D, C, iis.ravel(), jjs.ravel(), err_factor=1.0)
+    assert bad == 0, first
+    assert alo <= amax <= ahi
+
+
+def test_gemm_check_rejects_planted_errors(orc):
+    """Negative controls: a transposed operand, a dropped k term and a result off by a few ulps beyond
+    the bound are all caught."""
+    rng = np.random.default_rng(9)
+    m, n, k = 32, 32, 64
+    A, lda, B, ldb = _mk_case(orc, rng, 1, 0, 4, 4, m, n, k)
+    iis, jjs = [a.ravel() for a in np.meshgrid(np.arange(m), np.arange(n), indexing="ij")]
+    good = orc.Gemm(1, 0, m, n, k, 1.0, 4, A, lda, 4, B, ldb, ddt=3)
+    good.chain()
+    # 1. transposed operand: run the chain with transa flipped on the same bytes
+    wrong = orc.Gemm(0, 0, m, n, k, 1.0, 4, A, lda, 4, B, ldb, ddt=3)
+    wrong.chain()
+    assert good.check(wrong.D, None, iis, jjs)[0] > m * n // 2
+    # 2. a dropped term: zero one k column of A
+    A2 = A.copy()
+    A2[np.arange(m) * lda + 5] = 0
+    dropped = orc.Gemm(1, 0, m, n, k, 1.0, 4, A2, lda, 4, B, ldb, ddt=3)
+    dropped.chain()
+    assert good.check(dropped.D, None, iis, jjs)[0] > 0
+    # 3. one output moved by 2 * (bound + ulp)
+    D = good.D.copy()
+    ex, mag = good.exact(iis[:1], jjs[:1])
+    D[0] = np.float32(ex[0] + 2 * (2 * k * mag[0] * 2.0 ** -24) + abs(ex[0]) * 2.0 ** -22 + 1e-30)
+    assert good.check(D, None, iis, jjs)[0] == 1
+    # 4. the sign of alpha flipped
+    neg = orc.Gemm(1, 0, m, n, k, -1.0, 4, A, lda, 4, B, ldb, ddt=3)
+    neg.chain()
+    assert good.check(neg.D, None, iis, jjs)[0] > m * n // 2
+
+
+def test_gemm_fp8_output_and_accumulate(orc):
+    rng = np.random.default_rng(4)
+    m, n, k = 20, 12, 32
+    A, lda, B, ldb = _mk_case(orc, rng, 1, 0, 4, 0, m, n, k)
+    D0 = rng.uniform(-1, 1, m * n).astype(np.float32)
+    g = orc.Gemm(1, 0, m, n, k, 1.0, 4, A, lda, 0, B, ldb, beta=1.0, C=None, ddt=3, D=D0.copy(), ldd=m)
+    g.chain()
+    iis, jjs = [a.ravel() for a in np.meshgrid(np.arange(m), np.arange(n), indexing="ij")]
+    ex, _ = g.exact(iis, jjs)
+    np.testing.assert_allclose(g.D[jjs * m + iis], ex + D0[jjs * m + iis], rtol=1e-5, atol=1e-6)
+    q = orc.Gemm(1, 0, m, n, k, 1.0, 4, A, lda, 0, B, ldb, ddt=4, qscale=0.25)
+    amax = q.chain()
+    f32 = orc.Gemm(1, 0, m, n, k, 1.0, 4, A, lda, 0, B, ldb, ddt=3)
+    f32.chain()
+    assert np.array_equal(q.D, orc.encode(4, f32.D, 0.25))
+    assert amax == np.abs(f32.D).max()
+
+
+# ---- Adam -------------------------------------------------------------------------------------------
+def test_adam_closed_form_unit_moments(orc):
+    """beta1 = beta2 = 0, eps = 0, no bias correction, no decay: m = g, v = RN(g*g), and
+    u = g / sqrt(RN(g^2)) = +-1 exactly, so p_new = RN(p -+ lr)."""
+    rng = np.random.default_rng(2)
+    n = 10000
+    p = rng.standard_normal(n).astype(np.float32)
+    g = (rng.standard_normal(n).astype(np.float32) + np.float32(0.01))
+    m, v = np.zeros(n, np.float32), np.zeros(n, np.float32)
+    cfg = dict(lr=1e-3, beta1=0.0, beta2=0.0, eps=0.0, weight_decay=0.0, step=1, adamw=1, bias_correction=0,
+               grad_scale=1.0)
+    p0 = p.copy()
+    orc.adam(cfg, 3, p, 3, g, 3, m, v)
+    assert np.array_equal(m, g) and np.array_equal(v, g * g)
+    assert np.array_equal(p, p0 - np.sign(g).astype(np.float32) * np.float32(1e-3))
+
+
+@pytest.mark.parametrize("adamw", [1, 0])
+def test_adam_vs_torch_fp32(orc, adamw):
+    rng = np.random.default_rng(8)
+    n = 4096
+    p = rng.standard_normal(n).astype(np.float32)
+    tp = torch.nn.Parameter(torch.from_numpy(p.copy()))
+    opt = (torch.optim.AdamW if adamw else torch.optim.Adam)([tp], lr=1e-2, weight_decay=0.1, foreach=False)
+    m, v = np.zeros(n, np.float32), np.zeros(n, np.float32)
+    for step in range(1, 6):
+        g = rng.standard_normal(n).astype(np.float32)
+        tp.grad = torch.from_numpy(g.copy())
+        opt.step()
+        cfg = dict(lr=1e-2, beta1=0.9, beta2=0.999, eps=1e-8, weight_decay=0.1, step=step, adamw=adamw,
+                   bias_correction=1, grad_scale=1.0)
+        orc.adam(cfg, 3, p, 3, g, 3, m, v)
+    np.testing.assert_allclose(p, tp.detach().numpy(), rtol=1e-6, atol=1e-6)
+
+
+def test_adam_fp8_copy_and_amax(orc):
+    rng = np.random.default_rng(6)
+    n = 1000
+    p = orc.encode(1, rng.standard_normal(n).astype(np.float32))
+    g = orc.encode(2, rng.standard_normal(n).astype(np.float32) * np.float32(0.1))
+    m = orc.encode(1, rng.standard_normal(n).astype(np.float32) * np.float32(0.01))
+    v = orc.encode(1, np.abs(rng.standard_normal(n)).astype(np.float32) * np.float32(1e-4))
+    q = np.zeros(n, np.uint8)
+    cfg = dict(lr=1e-3, beta1=0.9, beta2=0.999, eps=1e-8, weight_decay=0.01, step=3, adamw=1, bias_correction=1,
+               grad_scale=0.5)
+    amax = orc.adam(cfg, 1, p, 2, g, 1, m, v, qdt=0, q=q, qscale=64.0)
+    pf = orc.decode(1, p)
+    # amax is max |p| of the FP32 values, before their BF16 rounding
+    assert abs(amax - np.abs(pf).max()) <= np.abs(pf).max() * 2.0 ** -8 and amax != np.abs(pf).max()
+    # the copy is taken from the FP32 value before its BF16 rounding: it agrees with the stored BF16
+    # value to within one E4M3 rounding step
+    ref = orc.encode(0, pf, 64.0)
+    assert (np.abs(orc.decode(0, q).astype(np.float64) - orc.decode(0, ref)) <=
+            np.abs(orc.decode(0, ref)) * 2.0 ** -3 + 2.0 ** -9).all()
