@@ -192,6 +192,14 @@ void orc_decode_batch(int t, const void *p, float *out, size_t n, float sinv) {
   for (size_t i = 0; i < n; ++i) out[i] = orc_load(t, p, i, sinv);
 }
 
+/* |v| folded into a running maximum; every NaN (quiet or signalling) is ignored, as the reference's
+ * device reduction ignores it (src/e5m2effma.cuh:192, fmaxf on the GPU returns the non-NaN operand).
+ * glibc's fmaxf is not used: it returns NaN for a signalling-NaN operand. */
+static inline float amax_fold(float m, float v) {
+  const float a = fabsf(v);
+  return a > m ? a : m;
+}
+
 /* amax commit of the reference: |v| max-reduced with fmaxf (NaN ignored), then an integer atomicMax
  * of the float bits into *amax, issued only for a positive partial maximum
  * (src/e5m2effma.cuh:190-195). */
@@ -260,7 +268,7 @@ float orc_cast(int tin, int tout, const void *src, void *dst, size_t count, floa
   float m = 0.f;
   for (size_t i = 0; i < count; ++i) {
     const float v = orc_load(tin, src, i, sinv);
-    m = fmaxf(m, fabsf(v));
+    m = amax_fold(m, v);
     orc_store(tout, dst, i, v, qscale);
   }
   return amax_merge(amax_in, m);
@@ -343,7 +351,7 @@ static void *chain_worker(void *arg) {
       for (int jj = 0; jj < nj; ++jj) {
         const int j = j0 + jj;
         const float v = orc_epilogue(g, i, j, acc[jj], c_value(g, Cp, i, j));
-        m = fmaxf(m, fabsf(v));
+        m = amax_fold(m, v);
         orc_store(g->ddt, g->D, (size_t)j * g->ldd + i, v, g->qscale);
       }
     }
@@ -496,7 +504,7 @@ float orc_adam(const orc_adam_config *cfg, size_t count, int pdt, void *p, int g
     orc_store(mdt, m, i, mm, 1.f);
     orc_store(mdt, v, i, vv, 1.f);
     if (q) q[i] = qdt == ORC_E5M2 ? orc_f32_to_e5m2(pp * qscale) : orc_f32_to_e4m3(pp * qscale);
-    mx = fmaxf(mx, fabsf(pp));
+    mx = amax_fold(mx, pp);
   }
   return q ? amax_merge(amax_in, mx) : amax_in;
 }

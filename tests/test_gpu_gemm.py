@@ -1,0 +1,188 @@
+"""Tiled e5ma_gemm on the GPU against the oracle's bound
+|acc - exact| <= 2 * k * 2^-24 * sum|a*b| (exact products, FP32 accumulation in another order than the
+reference's FFMA chain), with the epilogue applied to both ends of the interval (oracle
+orc_gemm_check).  Mirrors the reference's coverage (tests/test_gemm.cu:13-46): 16 dtype pairs x 4
+layouts, m / n tails, every output dtype, C of another dtype, accumulate, bias, outer scaling."""
+import itertools
+
+import numpy as np
+import pytest
+import torch
+
+import gpu_util as gu
+import oracle
+
+pytestmark = pytest.mark.gpu
+E5, E4, B16, F32, F16 = oracle.E5M2, oracle.E4M3, oracle.BF16, oracle.FP32, oracle.FP16
+OPERANDS = [E5, E4, B16, F32]
+LAYOUTS = [(1, 0), (0, 0), (0, 1), (1, 1)]
+
+
+@pytest.fixture(scope="module")
+def dev():
+    return torch.device("cuda:0")
+
+
+@pytest.mark.parametrize("adt,bdt", list(itertools.product(OPERANDS, OPERANDS)))
+@pytest.mark.parametrize("ta,tb", LAYOUTS)
+def test_pairs_and_layouts(dev, adt, bdt, ta, tb):
+    rng = np.random.default_rng(adt * 100 + bdt * 10 + ta * 2 + tb)
+    case = gu.GemmCase(rng, ta, tb, 67, 45, 80, adt, bdt, ddt=F32, alpha=1.25, sa=0.37, sb=1.9, beta=0.5, cdt=F32,
+                       biasdt=F32)
+    bad, first = case.run_and_check(dev)
+    assert bad == 0, first
+
+
+@pytest.mark.parametrize("ddt", [B16, F16, F32, E5, E4])
+@pytest.mark.parametrize("ta,tb", [(1, 0), (0, 0)])
+def test_output_dtypes_and_amax(dev, ddt, ta, tb):
+    rng = np.random.default_rng(ddt + 10 * ta)
+    qs = 0.25 if ddt in gu.FP8 else None
+    case = gu.GemmCase(rng, ta, tb, 96, 80, 128, E5, E4, ddt=ddt, sa=0.5, sb=0.75, qscale=qs, amax=True)
+    bad, first = case.run_and_check(dev)
+    assert bad == 0, first
+
+
+@pytest.mark.parametrize("cdt", [B16, F16, F32, E5, E4])
+def test_c_of_every_dtype(dev, cdt):
+    rng = np.random.default_rng(cdt)
+    case = gu.GemmCase(rng, 1, 0, 72, 40, 64, E4, E5, ddt=B16, beta=-0.75, cdt=cdt, csinv=0.5, biasdt=B16)
+    bad, first = case.run_and_check(dev)
+    assert bad == 0, first
+
+
+@pytest.mark.parametrize("adt,bdt", [(E5, E4), (E5, B16), (B16, F32)])
+def test_accumulate_into_fp32_main_grad(dev, adt, bdt):
+    """TE 'accumulate': C = NULL, beta = 1, FP32 D (reference src/gemm_e5m2effma.cu:83)."""
+    rng = np.random.default_rng(3)
+    case = gu.GemmCase(rng, 1, 0, 130, 70, 96, adt, bdt, ddt=F32, beta=1.0, cdt=None, biasdt=F32)
+    bad, first = case.run_and_check(dev)
+    assert bad == 0, first
+
+
+@pytest.mark.parametrize("ta,tb", LAYOUTS)
+def test_outer_scaling(dev, ta, tb):
+    rng = np.random.default_rng(ta * 2 + tb + 40)
+    m, n = 100, 52
+    sa = (0.25 + rng.integers(0, 1024, m) / 512).astype(np.float32)  # reference tests/test_util.h:96-97
+    sb = (0.25 + rng.integers(0, 1024, n) / 512).astype(np.float32)
+    case = gu.GemmCase(rng, ta, tb, m, n, 64, E5, E4, ddt=B16, alpha=0.5, sa=sa, sb=sb)
+    bad, first = case.run_and_check(dev)
+    assert bad == 0, first
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 9, 16), (31, 33, 16), (129, 130, 48), (255, 257, 1040), (64, 64, 0),
+                                   (200, 16, 4096)])
+@pytest.mark.parametrize("adt,bdt", [(E5, E5), (E4, B16), (F32, E5)])
+def test_shapes(dev, m, n, k, adt, bdt):
+    rng = np.random.default_rng(m + n + k)
+    case = gu.GemmCase(rng, 1, 0, m, n, k, adt, bdt, ddt=B16, sa=0.5, biasdt=F32)
+    bad, first = case.run_and_check(dev)
+    assert bad == 0, first
+
+
+@pytest.mark.parametrize("adt,bdt", [(E5, E5), (E5, E4), (E4, E5), (E4, E4), (E5, B16), (B16, E4)])
+def test_single_product_is_exact(dev, adt, bdt):
+    """k = 16 with one non-zero term per output: D (FP32) = a * b exactly for every pair of codes, so the
+    matrix cores' products are exact, subnormals included (reference docs/numerics.md:3-28)."""
+    m = n = 256
+    k = 16
+
+    def codes(dt):
+        if dt in gu.FP8:
+            c = np.arange(256, dtype=np.uint8)
+            bad = (c & 0x7C) == 0x7C if dt == E5 else (c & 0x7F) == 0x7F
+            c[bad] = 0
+            return c
+        rng = np.random.default_rng(1)
+        return oracle.encode(B16, rng.standard_normal(256).astype(np.float32))
+    a, b = codes(adt), codes(bdt)
+    A = np.zeros(k * m, gu.NPD[adt])
+    B = np.zeros(k * n, gu.NPD[bdt])
+    A[np.arange(m) * k + 5] = a
+    B[np.arange(n) * k + 5] = b
+    case = gu.GemmCase(None, 1, 0, m, n, k, adt, bdt, ddt=F32, pad=0, A=A, B=B)
+    s, D, _ = case.run(dev)
+    assert s == 0
+    va = oracle.decode(adt, a).astype(np.float64)
+    vb = oracle.decode(bdt, b).astype(np.float64)
+    want = np.outer(vb, va).astype(np.float32)  # [j][i]
+    got = D.reshape(n, case.ldd)[:, :m]
+    assert np.array_equal(got, want)
+
+
+def test_config1_512_row_major(dev):
+    """BASELINE config 1 shape through the C ABI: row-major a @ b, 512^3, E5M2 x E5M2 -> BF16, N(0,1)*4
+    inputs, issued column-major as out^T = b^T a^T (e5ma_gemm(N, N, 512, 512, 512, A := b, B := a))."""
+    rng = np.random.default_rng(0xE5A001)
+    case = gu.GemmCase(rng, 0, 0, 512, 512, 512, E5, E5, ddt=B16, pad=0, dist="normal", sigma=4.0, sa=1.0, sb=1.0)
+    bad, first = case.run_and_check(dev)
+    assert bad == 0, first
+
+
+@pytest.mark.parametrize("ta,tb", LAYOUTS)
+def test_large_sampled(dev, ta, tb):
+    rng = np.random.default_rng(77 + ta * 2 + tb)
+    case = gu.GemmCase(rng, ta, tb, 1024, 768, 2048, E5, E4, ddt=B16, dist="normal", sigma=8.0, sa=1 / 64,
+                       sb=1 / 64, pad=0)
+    s, D, _ = case.run(dev)
+    assert s == 0
+    bad, first = case.check(D, samples=8192, rng=rng)
+    assert bad == 0, first
+
+
+def test_inf_nan_operands_propagate(dev):
+    """FP8 operand Inf / NaN codes are outside the contract; the matrix cores read them as OCP Inf / NaN,
+    so an E5M2 output saturates (Inf -> 0x7B / 0xFB), NaN -> 0x7F, and amax (NaN ignored) becomes Inf
+    (BASELINE config 4 run 3 semantics)."""
+    rng = np.random.default_rng(12)
+    m, n, k = 64, 48, 64
+    case = gu.GemmCase(rng, 1, 0, m, n, k, E4, E5, ddt=E5, qscale=1.0, amax=True, pad=0, dist="normal", sigma=0.5)
+    B = case.B.copy()
+    B[5 * k + 3] = 0x7C   # +Inf in column 5
+    B[9 * k + 7] = 0xFC   # -Inf in column 9
+    B[20 * k + 1] = 0x7E  # NaN in column 20
+    case.B = B
+    s, D, amax = case.run(dev)
+    assert s == 0
+    bad, first = case.check(D)
+    assert bad == 0, first
+    assert amax == np.inf
+
+
+# ---- the FP8 matrix-core path (k >= 8192) ---------------------------------------------------------
+def test_f8_path_worst_case_groups(dev):
+    """Every group of 8 consecutive k holds one product 2^e and seven products just below 2^(e - 13),
+    which the FP8 matrix cores truncate to zero (the worst case of their accumulation).  At k = 8192 the
+    result must still satisfy the contract bound 2 * k * 2^-24 * sum|a*b|."""
+    rng = np.random.default_rng(8192)
+    m, n, k = 64, 32, 8192
+    E5c = lambda v: oracle.encode(E5, np.asarray(v, np.float32))
+    A = np.zeros((m, k), np.uint8)
+    groups = k // 8
+    e = rng.integers(0, 14, (m, groups)).astype(np.float32)  # small terms stay E5M2 normals
+    sign = np.where(rng.integers(0, 2, (m, groups)) == 1, -1.0, 1.0).astype(np.float32)
+    A[:, 0::8] = E5c(sign * 2.0 ** e)
+    for t in range(1, 8):
+        A[:, t::8] = E5c(sign * 1.75 * 2.0 ** (e - 14))
+    B = np.full((n, k), E5c([1.0])[0], np.uint8)
+    case = gu.GemmCase(None, 1, 0, m, n, k, E5, E5, ddt=F32, pad=0, A=A.ravel(), B=B.ravel())
+    bad, first = case.run_and_check(dev)
+    assert bad == 0, first
+
+
+@pytest.mark.parametrize("adt,bdt", [(E5, E5), (E5, E4), (E4, E5), (E4, E4)])
+def test_f8_path_uniform_codes(dev, adt, bdt):
+    rng = np.random.default_rng(adt * 10 + bdt + 8192)
+    case = gu.GemmCase(rng, 1, 0, 160, 96, 8192, adt, bdt, ddt=F32, alpha=0.5, sa=0.37, sb=1.9, biasdt=F32,
+                       beta=0.5, cdt=B16, pad=0)
+    bad, first = case.run_and_check(dev)
+    assert bad == 0, first
+
+
+@pytest.mark.parametrize("ta,tb", LAYOUTS)
+def test_f8_path_layouts(dev, ta, tb):
+    rng = np.random.default_rng(ta * 2 + tb + 8193)
+    case = gu.GemmCase(rng, ta, tb, 200, 136, 8192 + 16, E5, E4, ddt=E5, qscale=0.5, amax=True, sa=0.25, sb=2.0)
+    bad, first = case.run_and_check(dev)
+    assert bad == 0, first
