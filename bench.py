@@ -1,0 +1,264 @@
+"""Benchmark of the FP8 compute path on one MI355X (the workloads of BASELINE.json).
+
+Headline ("step" = one e5ma_gemm call): the 8192^3 E5M2 x E4M3 -> BF16 GEMM (TN, per-tensor
+scale_inv 1/64, inputs N(0,1)*8 with 0.01 % set to the largest finite value), reported in TFLOP/s and as
+a fraction of the FP8 dense matrix-core peak.  Secondary lines (same JSON object, "secondary"): the
+same GEMM with E5M2 x E5M2 and E5M2 x BF16 operands, GEMV 8192 x 8192 at batch 1 and 8 (weights rotated
+through 6 distinct buffers so the 256 MB Infinity Cache cannot serve them), the fused AdamW step over
+256M parameters (BF16 and FP32 state, E5M2 copy) and the 8192^2 FP32 -> E5M2 cast.
+
+Every rate is algorithmic work / kernel time, the kernel time taken with HIP events on the stream the
+kernels run on (torch's current stream) around K back-to-back calls.  cpu_baseline: the oracle's FP32
+FFMA-chain GEMM (oracle/e5ma_oracle.c, the reference's host emulation order) timed on this host on a
+slab of output rows and scaled to the full problem.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only gemm,gemv,adam,cast] [--no-cpu]
+"""
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+FP8_PEAK_TFLOPS = 5000.0    # MI355X dense FP8 matrix cores
+BF16_PEAK_TFLOPS = 2500.0   # dense BF16
+HBM_PEAK_GBS = 8000.0       # HBM3E
+E4M3, BF16, FP16, FP32, E5M2 = 0, 1, 2, 3, 4
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--only", default="gemm,gemv,adam,cast")
+    p.add_argument("--no-cpu", action="store_true")
+    return p.parse_args()
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+    from e5m2effma_amd import _lib
+
+    L = _lib.lib()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    stream = torch.cuda.current_stream()
+    sp = ctypes.c_void_p(stream.cuda_stream)
+    only = set(args.only.split(","))
+    K, W = args.steps, args.warmup
+    keep = []
+
+    def check(s, what):
+        if s != 0:
+            raise RuntimeError(f"{what}: {_lib.status_string(s)}: {_lib.last_error()}")
+
+    def f32(v):
+        t = torch.tensor([v], dtype=torch.float32, device=dev)
+        keep.append(t)
+        return t.data_ptr()
+
+    def quantize(x, fmt, scale=1.0):
+        """FP32 device tensor -> FP8 codes through e5ma_cast (RNE, satfinite)."""
+        out = torch.empty(x.numel(), dtype=torch.uint8, device=dev)
+        S = _lib.tensor(x.data_ptr(), FP32)
+        D = _lib.tensor(out.data_ptr(), fmt, None, f32(scale) if scale != 1.0 else None)
+        check(L.e5ma_cast(ctypes.byref(S), ctypes.byref(D), x.numel(), sp), "cast")
+        return out
+
+    def timed(fn, steps, warmup):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for i in range(steps):
+            fn(i)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / steps  # ms per call
+
+    out = {}
+    secondary = []
+    g = torch.Generator(device=dev)
+
+    # ---- GEMM 8192^3 ------------------------------------------------------------------------------
+    if "gemm" in only:
+        M = N = Kd = 8192
+        g.manual_seed(0xE5A003)
+        xa = torch.randn(M * Kd, device=dev, generator=g) * 8
+        xb = torch.randn(N * Kd, device=dev, generator=g) * 8
+        sat = torch.randint(0, M * Kd, (M * Kd // 10000,), device=dev, generator=g)
+        xa[sat] = 57344.0
+        xb[sat] = 57344.0
+        A8 = quantize(xa, E5M2)
+        B8 = {E4M3: quantize(xb, E4M3), E5M2: quantize(xb, E5M2)}
+        Bbf = xb.to(torch.bfloat16)
+        del xa, xb
+        D = torch.empty(M * N, dtype=torch.bfloat16, device=dev)
+        sinv = f32(1.0 / 64)
+        flop = 2.0 * M * N * Kd
+
+        def gemm_fn(bdt):
+            Bdata = B8[bdt] if bdt != BF16 else Bbf
+            At = _lib.tensor(A8.data_ptr(), E5M2, sinv)
+            Bt = _lib.tensor(Bdata.data_ptr(), bdt, sinv if bdt != BF16 else None)
+            Dt = _lib.tensor(D.data_ptr(), BF16)
+
+            def f(i=0):
+                check(L.e5ma_gemm(1, 0, M, N, Kd, 1.0, ctypes.byref(At), Kd, ctypes.byref(Bt), Kd, 0.0, None, 0,
+                                  ctypes.byref(Dt), M, None, sp), "gemm")
+            return f
+        ms = timed(gemm_fn(E4M3), K, W)
+        tf = flop / (ms * 1e-3) / 1e12
+        out["gemm"] = dict(ms=ms, tflops=tf)
+        for bdt, name, peak in ((E5M2, "E5M2xE5M2", FP8_PEAK_TFLOPS), (BF16, "E5M2xBF16", BF16_PEAK_TFLOPS)):
+            ms2 = timed(gemm_fn(bdt), max(3, K // 2), 2)
+            t2 = flop / (ms2 * 1e-3) / 1e12
+            secondary.append({"workload": f"gemm 8192^3 {name}->BF16 TN", "value": round(t2, 1), "unit": "TFLOP/s",
+                              "ms_per_call": round(ms2, 4),
+                              "roofline": {"bound": "mfma", "achieved": round(t2, 1), "peak": peak, "unit": "TFLOP/s",
+                                           "frac": round(t2 / peak, 4), "traffic": None}})
+        del A8, B8, Bbf, D
+
+    # ---- GEMV 8192^2, batch 1 and 8 -----------------------------------------------------------------
+    if "gemv" in only:
+        M = Kd = 8192
+        nbuf = 6
+        g.manual_seed(0xE5A002)
+        Ws, sas = [], []
+        for b in range(nbuf):
+            w = torch.randn(M * Kd, device=dev, generator=g) * 0.02
+            amax = w.abs().max().item()
+            Ws.append(quantize(w, E5M2, 57344.0 / amax))
+            sas.append(torch.full((M,), amax / 57344.0, dtype=torch.float32, device=dev))
+            del w
+        for n in (1, 8):
+            x = torch.randn(Kd * n, device=dev, generator=g).to(torch.bfloat16)
+            y = torch.empty(M * n, dtype=torch.bfloat16, device=dev)
+            descs = [(_lib.tensor(Ws[b].data_ptr(), E5M2, sas[b].data_ptr(), None, None, 1)) for b in range(nbuf)]
+            Bt = _lib.tensor(x.data_ptr(), BF16)
+            Dt = _lib.tensor(y.data_ptr(), BF16)
+
+            def f(i=0):
+                check(L.e5ma_gemm(1, 0, M, n, Kd, 1.0, ctypes.byref(descs[i % nbuf]), Kd, ctypes.byref(Bt), Kd, 0.0,
+                                  None, 0, ctypes.byref(Dt), M, None, sp), "gemv")
+            ms = timed(f, max(K, 30), W)
+            nbytes = M * Kd + M * 4 + Kd * n * 2 + M * n * 2  # weights, row scales, x, y
+            gbs = nbytes / (ms * 1e-3) / 1e9
+            secondary.append({"workload": f"gemv 8192x8192 E5M2 (row-wise scale_inv) x BF16 n={n} -> BF16",
+                              "value": round(gbs, 1), "unit": "GB/s", "ms_per_call": round(ms, 5),
+                              "bytes_per_call": nbytes,
+                              "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                                           "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None}})
+        del Ws, sas
+
+    # ---- AdamW 256M parameters ----------------------------------------------------------------------
+    if "adam" in only:
+        n = 256 * 1024 * 1024
+        for st, name in ((BF16, "BF16"), (FP32, "FP32")):
+            tdt = torch.bfloat16 if st == BF16 else torch.float32
+            g.manual_seed(0xE5A005)
+            p = (torch.randn(n, device=dev, generator=g) * 0.02).to(tdt)
+            gr = (torch.randn(n, device=dev, generator=g) * 1e-3).to(tdt)
+            m = torch.zeros(n, dtype=tdt, device=dev)
+            v = torch.zeros(n, dtype=tdt, device=dev)
+            q = torch.empty(n, dtype=torch.uint8, device=dev)
+            am = torch.zeros(1, dtype=torch.float32, device=dev)
+            qs = f32(57344.0 / 0.1)
+            P, G, Mo, V = (_lib.tensor(t.data_ptr(), st) for t in (p, gr, m, v))
+            Q = _lib.tensor(q.data_ptr(), E5M2, None, qs, am.data_ptr())
+            step = [0]
+
+            def f(i=0):
+                step[0] += 1
+                cfg = _lib.AdamConfig(1e-4, 0.9, 0.999, 1e-8, 0.01, step[0], 1, 1, 1.0)
+                check(L.e5ma_adam(ctypes.byref(cfg), n, ctypes.byref(P), ctypes.byref(G), ctypes.byref(Mo),
+                                  ctypes.byref(V), ctypes.byref(Q), sp), "adam")
+            ms = timed(f, 10, 2)
+            es = 2 if st == BF16 else 4
+            nbytes = n * (7 * es + 1)  # read p, g, m, v; write p, m, v; write the FP8 copy
+            gbs = nbytes / (ms * 1e-3) / 1e9
+            secondary.append({"workload": f"adamw 256M params {name} p/g/m/v + E5M2 copy", "value": round(gbs, 1),
+                              "unit": "GB/s", "ms_per_call": round(ms, 4), "bytes_per_call": nbytes,
+                              "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                                           "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None}})
+            del p, gr, m, v, q
+
+    # ---- cast 8192^2 FP32 -> E5M2 --------------------------------------------------------------------
+    if "cast" in only:
+        n = 8192 * 8192
+        nbuf = 2  # 2 x 268 MB of sources rotate past the Infinity Cache
+        g.manual_seed(0xE5A004)
+        srcs = [torch.randn(n, device=dev, generator=g) * 0.02 for _ in range(nbuf)]
+        dst = torch.empty(n, dtype=torch.uint8, device=dev)
+        am = torch.zeros(1, dtype=torch.float32, device=dev)
+        amax = srcs[0].abs().max().item()
+        descs = [_lib.tensor(s.data_ptr(), FP32) for s in srcs]
+        Dt = _lib.tensor(dst.data_ptr(), E5M2, None, f32(57344.0 / amax), am.data_ptr())
+
+        def f(i=0):
+            check(L.e5ma_cast(ctypes.byref(descs[i % nbuf]), ctypes.byref(Dt), n, sp), "cast")
+        ms = timed(f, max(K, 20), W)
+        nbytes = n * 5
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        secondary.append({"workload": "cast 8192x8192 FP32 -> E5M2 (scale, amax)", "value": round(gbs, 1),
+                          "unit": "GB/s", "ms_per_call": round(ms, 5), "bytes_per_call": nbytes,
+                          "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                       "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None}})
+        del srcs, dst
+
+    # ---- CPU baseline: the oracle's FFMA chain on a slab of the 8192^3 GEMM ---------------------------
+    cpu = None
+    if not args.no_cpu and "gemm" in only:
+        import numpy as np
+        import oracle
+        rng = np.random.default_rng(1)
+        Md = Nd = Kd = 8192
+        A = oracle.encode(E5M2, (rng.standard_normal(Kd * 64) * 8).astype(np.float32))
+        A = np.tile(A, Md // 64)  # the chain's cost does not depend on the values
+        B = oracle.encode(E4M3, (rng.standard_normal(Kd * 64) * 8).astype(np.float32))
+        B = np.tile(B, Nd // 64)
+        threads = max(1, min(16, os.cpu_count() or 1))
+        gm = oracle.Gemm(1, 0, Md, Nd, Kd, 1.0, E5M2, A, Kd, E4M3, B, Kd, sa=[1 / 64], sb=[1 / 64], ddt=BF16)
+        rows = 2
+        while True:
+            t0 = time.perf_counter()
+            gm.chain(rows=(0, rows), threads=threads)
+            dt = time.perf_counter() - t0
+            if dt > 2.0 or rows >= 64:
+                break
+            rows *= 2
+        cpu_tflops = 2.0 * rows * Nd * Kd / dt / 1e12
+        cpu = {"value": round(cpu_tflops, 6), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+               "sample": f"{rows} of 8192 output rows of the 8192^3 E5M2 x E4M3 GEMM, ascending-k FP32 fmaf chain "
+                         f"(oracle/e5ma_oracle.c, {threads} threads), rate scaled to the full problem"}
+
+    res = {"metric": "FP8 GEMM TFLOP/s @8192^3 (% FP8 peak); GEMV + AdamW HBM GB/s (% of 8 TB/s)",
+           "unit": "TFLOP/s", "n_gpus": 1, "steps": K, "warmup": W, "higher_is_better": True, "scaling": "weak",
+           "vs_baseline": None, "dtype": "fp8", "data": "synthetic"}
+    if "gemm" in out:
+        tf = out["gemm"]["tflops"]
+        res.update({"value": round(tf, 1), "ms_per_step": round(out["gemm"]["ms"], 4),
+                    "config": {"workload": "gemm 8192x8192x8192 E5M2 x E4M3 -> BF16, TN, scale_inv 1/64, alpha 1, "
+                                           "beta 0 (BASELINE config 3 shape, north-star pairing)"},
+                    "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": FP8_PEAK_TFLOPS,
+                                 "unit": "TFLOP/s", "frac": round(tf / FP8_PEAK_TFLOPS, 4), "traffic": None}})
+    else:
+        res.update({"value": None, "ms_per_step": None, "config": {"workload": "gemm not run (--only)"}})
+    res["cpu_baseline"] = cpu
+    res["secondary"] = secondary
+    print(json.dumps(res))
+
+
+if __name__ == "__main__":
+    main()
