@@ -32,7 +32,7 @@ __host__ __device__ constexpr int mode_of(int a, int b, int k) {
 // E8M0 block scale 2^0: the scaled f8f6f4 MFMA then computes the plain product
 constexpr int kNeutralScale = 127;
 // f8f6f4 operand format selector (cbsz for A, blgp for B): 0 = E4M3, 1 = E5M2
-template <int T> __host__ __device__ constexpr int mfma_fmt() { return T == E5MA_E5M2 ? 1 : 0; }
+template <int T> constexpr int kMfmaFmt = T == E5MA_E5M2 ? 1 : 0;
 
 // GEMM operand element idx of dtype T as an exact FP32 value.  FP8 codes decode as OCP values, the
 // way the matrix cores read them (Inf / NaN codes propagate).
@@ -111,6 +111,9 @@ __device__ __attribute__((noinline)) float epilogue_block(const dev::Epilogue &e
 
 }  // namespace gemm
 
+bool gemm_f8_tn_applies(int at, int bt, bool akc, bool bkc, int m, int n, int k);
+hipError_t launch_gemm_f8_tn(int at, int bt, const uint8_t *A, long long lda, const uint8_t *B, long long ldb, int m,
+                             int n, int k, const dev::Epilogue &e, hipStream_t s);
 hipError_t launch_gemm_generic(int at, int bt, bool akc, bool bkc, const uint8_t *A, long long lda, const uint8_t *B,
                                long long ldb, int m, int n, int k, const dev::Epilogue &e, hipStream_t s);
 

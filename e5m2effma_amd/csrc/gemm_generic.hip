@@ -169,8 +169,8 @@ __global__ __launch_bounds__(kThreads) void gemm_generic_kernel(const uint8_t *_
       for (int x = 0; x < 2; ++x)
 #pragma unroll
         for (int y = 0; y < 2; ++y)
-          acc[x][y] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fa[x], fb[y], acc[x][y], mfma_fmt<AT>(),
-                                                                      mfma_fmt<BT>(), 0, kNeutralScale, 0,
+          acc[x][y] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fa[x], fb[y], acc[x][y], kMfmaFmt<AT>,
+                                                                      kMfmaFmt<BT>, 0, kNeutralScale, 0,
                                                                       kNeutralScale);
     } else if constexpr (MODE == kModeH) {
 #pragma unroll
