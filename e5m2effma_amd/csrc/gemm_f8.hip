@@ -5,14 +5,17 @@
 //
 // Block tile 256 x 256, 4 waves (one per SIMD), each owning a 128 x 128 sub-tile held as 4 x 4
 // accumulator blocks of v_mfma_scale_f32_32x32x64_f8f6f4 (256 accumulator registers per lane).
-// K advances in stages of 64 bytes.  A 4-slot LDS ring (4 x 32 KiB) is filled by direct-to-LDS
-// loads (global_load_lds_dwordx4: 64 lanes x 16 bytes land contiguously, no VGPR staging) issued
-// three stages ahead; each stage costs one barrier.  The fragments are single-buffered (64 VGPRs
-// beside the 256 accumulator registers): each fragment register is refilled from stage s + 1 right
-// after the last MFMA of stage s that reads it, so LDS reads overlap the matrix cores.  LDS rows are 64 bytes; 16-byte chunk c of row r is stored at chunk
-// c ^ ((r >> 1 ^ r >> 3) & 3), which spreads any 8 (32 banks) or 16 (64 banks) consecutive rows of
-// a fragment read over distinct banks.  Tiles are ordered so that the 32 blocks an XCD runs at once
-// form a 4 x 8 patch of the output (A slices shared by 8 blocks, B slices by 4, in that XCD's L2).
+// K advances in stages of 64 bytes.  A 4-slot LDS ring (4 x 32 KiB, one object per slot and operand)
+// is filled by direct-to-LDS loads (global_load_lds_dwordx4: 64 lanes x 16 bytes land contiguously,
+// no VGPR staging) issued three stages ahead; each stage costs one barrier.  The fragments are
+// single-buffered (64 VGPRs beside the 256 accumulator registers) and the stage loop is unrolled by 4
+// so that ring slots are compile-time indices.  Within a stage the MFMAs, the fragment reads of the
+// next stage and the loads of stage s + 4 are interleaved.  LDS rows are 64 bytes; 16-byte chunk c of
+// row r is stored at chunk c ^ ((r >> 2) & 3): gfx950's LDS serves a ds_read_b128 16 lanes per
+// cycle over 64 banks (measured: a contiguous read takes 4 cycles, lanes l and l + 8 share a cycle,
+// l and l + 16 do not), and with this swizzle the fragment reads are conflict-free (measured).
+// Tiles are ordered so that the 32 blocks an XCD runs at once form a 4 x 8 patch of the output
+// (A slices shared by 8 blocks, B slices by 4, in that XCD's L2).
 #include "e5ma_host.hpp"
 #include "gemm_common.hpp"
 
@@ -45,7 +48,7 @@ template <int S> __device__ __forceinline__ uint8_t *lds_b() {
 }
 typedef __attribute__((address_space(1))) const void glob_cvoid;
 
-__device__ __forceinline__ int swz(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
+__device__ __forceinline__ int swz(int r) { return (r >> 2) & 3; }
 
 // s_waitcnt vmcnt(N) lgkmcnt(0), then s_barrier; the memory clobber keeps the compiler from moving
 // memory operations across it.  (__syncthreads would also wait for every outstanding global load.)
@@ -83,20 +86,21 @@ __device__ __forceinline__ void load_lds16(const uint8_t *src, const uint8_t *ld
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(l) : "memory", "m0");
 }
 
-// this wave's share of one stage: 4 x 1 KiB of A rows and of B rows into LDS slot SLOT
+// load q (of kLoadsPerWave) of this wave's share of one stage: 1 KiB of A rows and 1 KiB of B rows
+// (16 rows each) into LDS slot SLOT
 template <int SLOT>
-__device__ __forceinline__ void issue_stage(const TileArgs &t, int kb, int i0, int j0, int wave, int lane) {
-  uint8_t *sa = lds_a<SLOT>(), *sb = lds_b<SLOT>();
-  const int rsub = lane >> 2, cpos = lane & 3;
+__device__ __forceinline__ void issue_load(const TileArgs &t, int kb, int i0, int j0, int wave, int lane, int q) {
+  const int blk = wave * kLoadsPerWave + q;
+  const int r = blk * 16 + (lane >> 2);
+  const int c = (lane & 3) ^ swz(r);
+  const int ra = min(i0 + r, t.m - 1), rb = min(j0 + r, t.n - 1);
+  load_lds16(t.A + (long long)ra * t.lda + kb + 16 * c, lds_a<SLOT>() + blk * 1024);
+  load_lds16(t.B + (long long)rb * t.ldb + kb + 16 * c, lds_b<SLOT>() + blk * 1024);
+}
+template <int SLOT> __device__ __forceinline__ void issue_stage(const TileArgs &t, int kb, int i0, int j0, int wave,
+                                                               int lane) {
 #pragma unroll
-  for (int q = 0; q < kLoadsPerWave; ++q) {
-    const int blk = wave * kLoadsPerWave + q;  // 16 rows per 1 KiB block
-    const int r = blk * 16 + rsub;
-    const int c = cpos ^ swz(r);
-    const int ra = min(i0 + r, t.m - 1), rb = min(j0 + r, t.n - 1);
-    load_lds16(t.A + (long long)ra * t.lda + kb + 16 * c, sa + blk * 1024);
-    load_lds16(t.B + (long long)rb * t.ldb + kb + 16 * c, sb + blk * 1024);
-  }
+  for (int q = 0; q < kLoadsPerWave; ++q) issue_load<SLOT>(t, kb, i0, j0, wave, lane, q);
 }
 
 // fragments of one 32-row block of an operand stage: lane l holds the 32 K bytes
@@ -112,14 +116,14 @@ __device__ __forceinline__ v8i read_frag(const uint8_t *s, int r0, int lane) {
 
 // Stage s (= SLOT mod 4) of the K loop; a / b hold stage s's fragments.  WAITN: global loads this
 // wave may leave in flight when stage s + 1 must have landed; NEXT: a stage s + 1 exists; ISSUE:
-// stage s + 4 exists.  After the barrier, the slot of stage s is refilled with stage s + 4, and the
-// 16 MFMAs of stage s are issued with the fragment registers refilled from stage s + 1 right after
-// their last use.
+// stage s + 4 exists.  After the barrier the 16 MFMAs of stage s are issued; the loads of stage s + 4
+// into stage s's slot (free: every wave read it before the barrier) go out one pair after every
+// fourth MFMA, and each fragment register is refilled from stage s + 1 right after its last use, with
+// the LDS reads spread one per MFMA.  (Issuing the 8 loads as one burst stalled the MFMA stream.)
 template <int WAITN, bool NEXT, bool ISSUE, int SLOT, int AT, int BT>
 __device__ __forceinline__ void f8_stage(const TileArgs &t, int s, int i0, int j0, int wave, int lane, int wm, int wn,
                                          v8i (&a)[4], v8i (&b)[4], v16f (&acc)[4][4]) {
   if constexpr (NEXT) wait_barrier<WAITN>();
-  if constexpr (ISSUE) issue_stage<SLOT>(t, (s + 4) * kBK, i0, j0, wave, lane);
   const uint8_t *na = lds_a<(SLOT + 1) & 3>(), *nb = lds_b<(SLOT + 1) & 3>();
 #pragma unroll
   for (int x = 0; x < 4; ++x) {
@@ -127,6 +131,9 @@ __device__ __forceinline__ void f8_stage(const TileArgs &t, int s, int i0, int j
     for (int y = 0; y < 4; ++y) {
       acc[x][y] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a[x], b[y], acc[x][y], kMfmaFmt<AT>, kMfmaFmt<BT>, 0,
                                                                   kNeutralScale, 0, kNeutralScale);
+      if constexpr (ISSUE) {
+        if (y == 1) issue_load<SLOT>(t, (s + 4) * kBK, i0, j0, wave, lane, x);
+      }
       if constexpr (NEXT) {
         if (x == 3) b[y] = read_frag(nb, 128 * wn + 32 * y, lane);
       }
@@ -304,3 +311,4 @@ hipError_t launch_gemm_f8_tn(int at, int bt, const uint8_t *A, long long lda, co
 }
 
 }  // namespace e5ma
+
