@@ -80,7 +80,8 @@ __device__ __forceinline__ void tile_of(int b, int tiles_m, int tiles_n, int &tm
 // Written as inline asm so that the compiler's wait-count pass does not treat it as an LDS store it
 // must wait for before every later LDS read: this kernel orders the ring slots itself (wait_barrier
 // with explicit vmcnt).  Vector-memory operations complete in issue order, so these extra loads in
-// flight can only make a wait the compiler emits for its own loads more conservative.
+// flight can only make a wait the compiler emits for its own loads more conservative.  It sets m0
+// itself; the compiler emits no other m0 use in this file (checked in the generated code).
 __device__ __forceinline__ void load_lds16(const uint8_t *src, const uint8_t *lds) {
   const uint32_t l = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t *)lds);
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(l) : "memory", "m0");

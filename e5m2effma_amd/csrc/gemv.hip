@@ -66,6 +66,30 @@ __device__ __forceinline__ float wave_sum(float x) {
   return x;
 }
 
+
+// Epilogue operands of the one output lane `lane` finishes (row r = lane / NB, column j = lane % NB),
+// fetched when the kernel starts: loaded after the reduction they would add a full memory latency to
+// the end of every wave.  finish() applies the epilogue in the documented order (as epi_value does).
+template <int NB> struct GemvOut {
+  int r, j;
+  float s, bias, c;
+  __device__ __forceinline__ void fetch(const Epilogue &e, const EpiState &st, int row0, int m, int R, int lane) {
+    r = lane / NB;
+    j = lane - r * NB;
+    const int i = min(row0 + r, m - 1);
+    s = epi_scale(e, st, i, j);
+    bias = e.bias ? load_any(e.bias_dtype, e.bias, (size_t)i, 1.f) : 0.f;
+    c = e.beta != 0.f ? load_any(e.c_dtype, e.c, (size_t)j * e.ldc + i, st.csinv) : 0.f;
+    if (r >= R) r = -1;
+  }
+  __device__ __forceinline__ float finish(const Epilogue &e, float acc) const {
+    float v = acc * s;
+    if (e.bias) v = v + bias;
+    if (e.beta != 0.f) v = __builtin_fmaf(e.beta, c, v);
+    return v;
+  }
+};
+
 template <int AT, int BT, int NB, int R, int U>
 __global__ __launch_bounds__(kThreads) void gemv_kernel(const uint8_t *__restrict__ A, long long lda,
                                                         const uint8_t *__restrict__ B, long long ldb, int m, int k,
@@ -74,6 +98,9 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const uint8_t *__restric
   const int lane = threadIdx.x & 63;
   const int row0 = (blockIdx.x * kWaves + (threadIdx.x >> 6)) * R;
   const int nch = k >> 4;  // 16-byte chunks per row
+  const EpiState st = epi_begin(e);
+  GemvOut<NB> out;
+  out.fetch(e, st, row0, m, R, lane);
   float acc[R][NB];
 #pragma unroll
   for (int r = 0; r < R; ++r)
@@ -117,25 +144,280 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const uint8_t *__restric
     }
   }
 
-  const EpiState st = epi_begin(e);
   float mine = 0.f;
-  int my_r = -1, my_j = 0;
 #pragma unroll
   for (int r = 0; r < R; ++r)
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
-      const float s = wave_sum(acc[r][j]);
-      if (lane == r * NB + j) {
-        mine = s;
-        my_r = r;
-        my_j = j;
-      }
+      const float sum = wave_sum(acc[r][j]);
+      if (lane == r * NB + j) mine = sum;
     }
   float mx = 0.f;
-  if (my_r >= 0 && row0 + my_r < m) {
-    const int i = row0 + my_r;
-    const float v = epi_value(e, st, i, my_j, mine);
-    store_any(e.d_dtype, e.d, (size_t)my_j * e.ldd + i, v, st.qscale);
+  if (out.r >= 0 && row0 + out.r < m) {
+    const int i = row0 + out.r;
+    const float v = out.finish(e, mine);
+    store_any(e.d_dtype, e.d, (size_t)out.j * e.ldd + i, v, st.qscale);
+    mx = amax_fold(0.f, v);
+  }
+  if (e.amax) amax_commit_block(e.amax, mx, red);
+}
+
+
+// ---- dot-product kernel for x in BF16, E5M2 or E4M3 --------------------------------------------
+// Launch shape (rows per wave R, chunks per lane and batch U) for n <= 2 and for wider x.
+#ifndef E5MA_GEMV_R_NARROW
+#define E5MA_GEMV_R_NARROW 2
+#endif
+#ifndef E5MA_GEMV_U_NARROW
+#define E5MA_GEMV_U_NARROW 4
+#endif
+#ifndef E5MA_GEMV_R_WIDE
+#define E5MA_GEMV_R_WIDE 2
+#endif
+#ifndef E5MA_GEMV_U_WIDE
+#define E5MA_GEMV_U_WIDE 4
+#endif
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// 4 FP8 codes of a dword -> 2 packed BF16 pairs, exactly (every finite FP8 value is a BF16 value)
+template <int T> __device__ __forceinline__ void fp8x4_to_bf16(uint32_t w, bf16x2 &lo, bf16x2 &hi) {
+  if constexpr (T == E5MA_E5M2) {
+    lo = __builtin_amdgcn_cvt_scalef32_pk_bf16_bf8((int)w, 1.0f, false);
+    hi = __builtin_amdgcn_cvt_scalef32_pk_bf16_bf8((int)w, 1.0f, true);
+  } else {
+    lo = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)w, 1.0f, false);
+    hi = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)w, 1.0f, true);
+  }
+}
+
+// x values 16c .. 16c + 15 of column j as 8 BF16 pairs (raw for BF16 x, converted for FP8 x)
+template <int BT> struct XChunk {
+  static constexpr int kDw = is_fp8(BT) ? 4 : 8;  // dwords loaded per chunk
+  uint32_t w[kDw];
+  __device__ __forceinline__ void load(const uint8_t *B, long long ldb, int j, int c) {
+    const u32x4 *p = (const u32x4 *)(B + ((long long)j * ldb + 16 * c) * elem_bytes(BT));
+#pragma unroll
+    for (int h = 0; h < kDw / 4; ++h) {
+      const u32x4 q = p[h];
+      w[4 * h] = q[0]; w[4 * h + 1] = q[1]; w[4 * h + 2] = q[2]; w[4 * h + 3] = q[3];
+    }
+  }
+  __device__ __forceinline__ void pairs(bf16x2 xp[8], bool valid) const {
+    if constexpr (is_fp8(BT)) {
+#pragma unroll
+      for (int d = 0; d < 4; ++d) fp8x4_to_bf16<BT>(valid ? w[d] : 0u, xp[2 * d], xp[2 * d + 1]);
+    } else {
+#pragma unroll
+      for (int d = 0; d < 8; ++d) xp[d] = __builtin_bit_cast(bf16x2, valid ? w[d] : 0u);
+    }
+  }
+};
+
+// Each wave64 owns R rows.  A batch issues every weight load of U chunks per lane (non-temporal
+// dwordx4, branch-free: chunk indices are clamped and chunks past the row end are zeroed after the
+// load), then the x chunks; the compute follows the loads as they land (they complete in order).  Per
+// 16 weights and row: 8 v_cvt_scalef32_pk_bf16_{bf8,fp8} and 8 v_dot2_f32_bf16 (products exact,
+// FP32 accumulation), with x shared by the R rows.
+template <int AT, int BT, int NB, int R, int U>
+// (A and B are not __restrict__: loads through restrict pointers may be moved across the fence
+// that keeps the x loads ahead of the weight loads.)
+__global__ __launch_bounds__(kThreads) void gemv_dot_kernel(const uint8_t *A, long long lda, const uint8_t *B,
+                                                            long long ldb, int m, int k, Epilogue e) {
+  __shared__ float red[kWaves];
+  const int lane = threadIdx.x & 63;
+  const int row0 = (blockIdx.x * kWaves + (threadIdx.x >> 6)) * R;
+  const int nch = k >> 4;
+  const EpiState st = epi_begin(e);
+  GemvOut<NB> out;
+  out.fetch(e, st, row0, m, R, lane);
+  const uint8_t *arow[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) arow[r] = A + (long long)min(row0 + r, m - 1) * lda;  // rows past m: never stored
+  float acc[R][NB];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int j = 0; j < NB; ++j) acc[r][j] = 0.f;
+
+  // x up front (NB <= 2): its loads are then older than the weight loads, so the first chunk's
+  // products can start as soon as its weights land (vector-memory loads complete in order)
+  constexpr bool kXUp = NB <= 2;
+  for (int c0 = lane; c0 < nch; c0 += 64 * U) {
+    XChunk<BT> xup[kXUp ? U : 1][kXUp ? NB : 1];
+    if constexpr (kXUp) {
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int j = 0; j < NB; ++j) xup[u][j].load(B, ldb, j, min(c0 + 64 * u, nch - 1));
+      asm volatile("" ::: "memory");
+    }
+    u32x4 wa[U][R];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int c = min(c0 + 64 * u, nch - 1);
+#pragma unroll
+      for (int r = 0; r < R; ++r) wa[u][r] = __builtin_nontemporal_load((const u32x4 *)(arow[r] + 16 * c));
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int c = c0 + 64 * u;
+      const bool valid = c < nch;
+      const int cc = valid ? c : nch - 1;
+#pragma unroll
+      for (int j = 0; j < NB; ++j) {
+        XChunk<BT> xc;
+        if constexpr (kXUp) xc = xup[u][j];
+        else xc.load(B, ldb, j, cc);
+        bf16x2 xp[8];
+        xc.pairs(xp, valid);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+#pragma unroll
+          for (int d = 0; d < 4; ++d) {
+            bf16x2 lo, hi;
+            fp8x4_to_bf16<AT>(valid ? wa[u][r][d] : 0u, lo, hi);
+            acc[r][j] = __builtin_amdgcn_fdot2_f32_bf16(lo, xp[2 * d], acc[r][j], false);
+            acc[r][j] = __builtin_amdgcn_fdot2_f32_bf16(hi, xp[2 * d + 1], acc[r][j], false);
+          }
+        }
+      }
+    }
+  }
+
+  float mine = 0.f;
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      const float sum = wave_sum(acc[r][j]);
+      if (lane == r * NB + j) mine = sum;
+    }
+  float mx = 0.f;
+  if (out.r >= 0 && row0 + out.r < m) {
+    const int i = row0 + out.r;
+    const float v = out.finish(e, mine);
+    store_any(e.d_dtype, e.d, (size_t)out.j * e.ldd + i, v, st.qscale);
+    mx = amax_fold(0.f, v);
+  }
+  if (e.amax) amax_commit_block(e.amax, mx, red);
+}
+
+// ---- x staged in LDS by direct-to-LDS loads (n <= 2, k * n * bytes(x) <= kXLds) ----------------
+constexpr int kXLds = 32768;
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+// one direct-to-LDS load: 16 bytes per lane from src to lds + 16 * lane (lds wave-uniform); inline asm,
+// so that it is ordered with the barrier asm below and not counted by the compiler's wait-count pass.
+// It sets m0 itself; the compiler emits no other m0 use in this file (checked in the generated code).
+__device__ __forceinline__ void gemv_load_lds16(const uint8_t *src, const uint8_t *lds) {
+  const uint32_t l = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t *)lds);
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(l) : "memory", "m0");
+}
+
+// x values 16c .. 16c + 15 of column j from the LDS copy (column j at xs + j * k * bytes(x))
+template <int BT> __device__ __forceinline__ void xlds_pairs(const uint8_t *xs, int k, int j, int c, bool valid,
+                                                            bf16x2 xp[8]) {
+  const uint8_t *p = xs + ((long long)j * k + 16 * c) * elem_bytes(BT);
+  XChunk<BT> xc;
+#pragma unroll
+  for (int h = 0; h < XChunk<BT>::kDw / 4; ++h) {
+    const uint4 q = ((const uint4 *)p)[h];
+    xc.w[4 * h] = q.x; xc.w[4 * h + 1] = q.y; xc.w[4 * h + 2] = q.z; xc.w[4 * h + 3] = q.w;
+  }
+  xc.pairs(xp, valid);
+}
+
+// As gemv_dot_kernel, but the block first copies x into LDS with direct-to-LDS loads (issued before
+// the weight loads, so they complete first), then waits only for those, so x never occupies the
+// vector-memory pipe again and the weights stream alone.
+// 256-thread blocks, 2 rows and 4 chunks per lane and batch (measured best of 1 / 2 / 4 rows, 4 / 8
+// chunks and 256 / 1024-thread blocks on the 8192 x 8192 batch-1 shape)
+constexpr int kXThreads = 256, kXWaves = kXThreads / 64;
+template <int AT, int BT, int NB, int R, int U>
+__global__ __launch_bounds__(kXThreads) void gemv_xlds_kernel(const uint8_t *A, long long lda, const uint8_t *B,
+                                                             long long ldb, int m, int k, Epilogue e) {
+  __shared__ __attribute__((aligned(1024))) uint8_t xs[kXLds];
+  __shared__ float red[kXWaves];
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int row0 = (blockIdx.x * kXWaves + wave) * R;
+  const int nch = k >> 4;
+  const EpiState st = epi_begin(e);
+  GemvOut<NB> out;
+  out.fetch(e, st, row0, m, R, lane);
+  const int colbytes = k * elem_bytes(BT), xtotal = colbytes * NB;
+  // x: 1 KiB per wave and step; source offsets past the end are clamped (the bytes they land on are
+  // never read)
+  constexpr int kSteps = kXLds / (1024 * kXWaves);
+#pragma unroll
+  for (int q = 0; q < kSteps; ++q) {
+    const int blk = q * kXWaves + wave;
+    if (blk * 1024 < xtotal) {  // wave-uniform
+      const int o = min(blk * 1024 + 16 * lane, xtotal - 16);
+      const int j = o / colbytes, w = o - j * colbytes;
+      gemv_load_lds16(B + (long long)j * ldb * elem_bytes(BT) + w, xs + blk * 1024);
+    }
+  }
+  const uint8_t *arow[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) arow[r] = A + (long long)min(row0 + r, m - 1) * lda;
+  float acc[R][NB];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int j = 0; j < NB; ++j) acc[r][j] = 0.f;
+
+  bool first = true;
+  for (int c0 = lane; c0 < nch; c0 += 64 * U) {
+    u32x4 wa[U][R];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int c = min(c0 + 64 * u, nch - 1);
+#pragma unroll
+      for (int r = 0; r < R; ++r) wa[u][r] = __builtin_nontemporal_load((const u32x4 *)(arow[r] + 16 * c));
+    }
+    if (first) {
+      // x landed (the U * R weight loads just issued may stay in flight), visible to the whole block
+      asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(U * R) : "memory");
+      first = false;
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int c = c0 + 64 * u;
+      const bool valid = c < nch;
+      const int cc = valid ? c : nch - 1;
+#pragma unroll
+      for (int j = 0; j < NB; ++j) {
+        bf16x2 xp[8];
+        xlds_pairs<BT>(xs, k, j, cc, valid, xp);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+#pragma unroll
+          for (int d = 0; d < 4; ++d) {
+            bf16x2 lo, hi;
+            fp8x4_to_bf16<AT>(valid ? wa[u][r][d] : 0u, lo, hi);
+            acc[r][j] = __builtin_amdgcn_fdot2_f32_bf16(lo, xp[2 * d], acc[r][j], false);
+            acc[r][j] = __builtin_amdgcn_fdot2_f32_bf16(hi, xp[2 * d + 1], acc[r][j], false);
+          }
+        }
+      }
+    }
+  }
+  if (first) asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");  // no chunk: still drain and sync
+
+  float mine = 0.f;
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      const float sum = wave_sum(acc[r][j]);
+      if (lane == r * NB + j) mine = sum;
+    }
+  float mx = 0.f;
+  if (out.r >= 0 && row0 + out.r < m) {
+    const int i = row0 + out.r;
+    const float v = out.finish(e, mine);
+    store_any(e.d_dtype, e.d, (size_t)out.j * e.ldd + i, v, st.qscale);
     mx = amax_fold(0.f, v);
   }
   if (e.amax) amax_commit_block(e.amax, mx, red);
@@ -144,11 +426,22 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const uint8_t *__restric
 template <int AT, int BT, int NB>
 hipError_t gemv_n(const uint8_t *A, long long lda, const uint8_t *B, long long ldb, int m, int k, const Epilogue &e,
                   hipStream_t s) {
-  constexpr int R = NB <= 2 ? 4 : 2;
-  constexpr int U = NB <= 2 ? 4 : 2;
-  const int rows_per_block = kWaves * R;
-  const int grid = (m + rows_per_block - 1) / rows_per_block;
-  gemv_kernel<AT, BT, NB, R, U><<<grid, kThreads, 0, s>>>(A, lda, B, ldb, m, k, e);
+  if constexpr (BT != E5MA_FP32 && NB <= 2) {
+    constexpr int R = E5MA_GEMV_R_NARROW, U = E5MA_GEMV_U_NARROW;
+    const int grid = (m + kWaves * R - 1) / (kWaves * R);
+    if ((long long)k * NB * elem_bytes(BT) <= kXLds) {
+      constexpr int RX = 2, UX = 4;
+      const int gx = (m + kXWaves * RX - 1) / (kXWaves * RX);
+      gemv_xlds_kernel<AT, BT, NB, RX, UX><<<gx, kXThreads, 0, s>>>(A, lda, B, ldb, m, k, e);
+    } else
+      gemv_dot_kernel<AT, BT, NB, R, U><<<grid, kThreads, 0, s>>>(A, lda, B, ldb, m, k, e);
+  } else {  // FP32 x is not a BF16 value, and for wider x the FP32 FMA kernel measured faster
+    constexpr int R = NB <= 2 ? 4 : 2;
+    constexpr int U = NB <= 2 ? 4 : 2;
+    const int rows_per_block = kWaves * R;
+    const int grid = (m + rows_per_block - 1) / rows_per_block;
+    gemv_kernel<AT, BT, NB, R, U><<<grid, kThreads, 0, s>>>(A, lda, B, ldb, m, k, e);
+  }
   return hipGetLastError();
 }
 
