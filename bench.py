@@ -8,11 +8,15 @@ through 6 distinct buffers so the 256 MB Infinity Cache cannot serve them), the 
 256M parameters (BF16 and FP32 state, E5M2 copy) and the 8192^2 FP32 -> E5M2 cast.
 
 Every rate is algorithmic work / kernel time, the kernel time taken with HIP events on the stream the
-kernels run on (torch's current stream) around K back-to-back calls.  cpu_baseline: the oracle's FP32
+kernels run on (torch's current stream) around K back-to-back calls.  "copy" times torch's device copy
+of 1 GiB: the streaming rate this GPU reaches in practice, and the known-size kernel the HBM counters
+are calibrated on.  roofline.traffic (HBM bytes per launch) comes from profiles/hbm_traffic.json, the
+rocprofv3 FETCH_SIZE / WRITE_SIZE counters of each workload's kernel scaled by the copy's
+calibration; null where no counter run covers the workload.  cpu_baseline: the oracle's FP32
 FFMA-chain GEMM (oracle/e5ma_oracle.c, the reference's host emulation order) timed on this host on a
 slab of output rows and scaled to the full problem.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only gemm,gemv,adam,cast] [--no-cpu]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only gemm,gemv,adam,cast,copy] [--no-cpu]
 """
 import argparse
 import ctypes
@@ -28,6 +32,16 @@ FP8_PEAK_TFLOPS = 5000.0    # MI355X dense FP8 matrix cores
 BF16_PEAK_TFLOPS = 2500.0   # dense BF16
 HBM_PEAK_GBS = 8000.0       # HBM3E
 E4M3, BF16, FP16, FP32, E5M2 = 0, 1, 2, 3, 4
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic.json")
+
+
+def traffic_table():
+    """Workload id -> HBM bytes per launch, from the committed counter summary (empty if absent)."""
+    try:
+        with open(TRAFFIC_FILE) as fh:
+            return {k: v["hbm_bytes_per_launch"] for k, v in json.load(fh)["workloads"].items()}
+    except (OSError, KeyError, ValueError):
+        return {}
 
 
 def parse():
@@ -35,7 +49,7 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=5)
-    p.add_argument("--only", default="gemm,gemv,adam,cast")
+    p.add_argument("--only", default="gemm,gemv,adam,cast,copy")
     p.add_argument("--no-cpu", action="store_true")
     return p.parse_args()
 
@@ -90,6 +104,11 @@ def main():
     out = {}
     secondary = []
     g = torch.Generator(device=dev)
+    traffic = traffic_table()
+
+    def roof(bound, achieved, peak, unit, wid):
+        return {"bound": bound, "achieved": round(achieved, 1), "peak": peak, "unit": unit,
+                "frac": round(achieved / peak, 4), "traffic": traffic.get(wid)}
 
     # ---- GEMM 8192^3 ------------------------------------------------------------------------------
     if "gemm" in only:
@@ -124,10 +143,9 @@ def main():
         for bdt, name, peak in ((E5M2, "E5M2xE5M2", FP8_PEAK_TFLOPS), (BF16, "E5M2xBF16", BF16_PEAK_TFLOPS)):
             ms2 = timed(gemm_fn(bdt), max(3, K // 2), 2)
             t2 = flop / (ms2 * 1e-3) / 1e12
-            secondary.append({"workload": f"gemm 8192^3 {name}->BF16 TN", "value": round(t2, 1), "unit": "TFLOP/s",
-                              "ms_per_call": round(ms2, 4),
-                              "roofline": {"bound": "mfma", "achieved": round(t2, 1), "peak": peak, "unit": "TFLOP/s",
-                                           "frac": round(t2 / peak, 4), "traffic": None}})
+            secondary.append({"workload": f"gemm 8192^3 {name}->BF16 TN", "id": f"gemm_8192_{name.lower()}",
+                              "value": round(t2, 1), "unit": "TFLOP/s", "ms_per_call": round(ms2, 4),
+                              "roofline": roof("mfma", t2, peak, "TFLOP/s", f"gemm_8192_{name.lower()}")})
         del A8, B8, Bbf, D
 
     # ---- GEMV 8192^2, batch 1 and 8 -----------------------------------------------------------------
@@ -156,10 +174,9 @@ def main():
             nbytes = M * Kd + M * 4 + Kd * n * 2 + M * n * 2  # weights, row scales, x, y
             gbs = nbytes / (ms * 1e-3) / 1e9
             secondary.append({"workload": f"gemv 8192x8192 E5M2 (row-wise scale_inv) x BF16 n={n} -> BF16",
-                              "value": round(gbs, 1), "unit": "GB/s", "ms_per_call": round(ms, 5),
-                              "bytes_per_call": nbytes,
-                              "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
-                                           "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None}})
+                              "id": f"gemv_8192_n{n}", "value": round(gbs, 1), "unit": "GB/s",
+                              "ms_per_call": round(ms, 5), "bytes_per_call": nbytes,
+                              "roofline": roof("hbm", gbs, HBM_PEAK_GBS, "GB/s", f"gemv_8192_n{n}")})
         del Ws, sas
 
     # ---- AdamW 256M parameters ----------------------------------------------------------------------
@@ -188,10 +205,10 @@ def main():
             es = 2 if st == BF16 else 4
             nbytes = n * (7 * es + 1)  # read p, g, m, v; write p, m, v; write the FP8 copy
             gbs = nbytes / (ms * 1e-3) / 1e9
-            secondary.append({"workload": f"adamw 256M params {name} p/g/m/v + E5M2 copy", "value": round(gbs, 1),
-                              "unit": "GB/s", "ms_per_call": round(ms, 4), "bytes_per_call": nbytes,
-                              "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
-                                           "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None}})
+            secondary.append({"workload": f"adamw 256M params {name} p/g/m/v + E5M2 copy",
+                              "id": f"adamw_256m_{name.lower()}", "value": round(gbs, 1), "unit": "GB/s",
+                              "ms_per_call": round(ms, 4), "bytes_per_call": nbytes,
+                              "roofline": roof("hbm", gbs, HBM_PEAK_GBS, "GB/s", f"adamw_256m_{name.lower()}")})
             del p, gr, m, v, q
 
     # ---- cast 8192^2 FP32 -> E5M2 --------------------------------------------------------------------
@@ -211,11 +228,26 @@ def main():
         ms = timed(f, max(K, 20), W)
         nbytes = n * 5
         gbs = nbytes / (ms * 1e-3) / 1e9
-        secondary.append({"workload": "cast 8192x8192 FP32 -> E5M2 (scale, amax)", "value": round(gbs, 1),
-                          "unit": "GB/s", "ms_per_call": round(ms, 5), "bytes_per_call": nbytes,
-                          "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                                       "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None}})
+        secondary.append({"workload": "cast 8192x8192 FP32 -> E5M2 (scale, amax)", "id": "cast_8192sq_fp32_e5m2",
+                          "value": round(gbs, 1), "unit": "GB/s", "ms_per_call": round(ms, 5), "bytes_per_call": nbytes,
+                          "roofline": roof("hbm", gbs, HBM_PEAK_GBS, "GB/s", "cast_8192sq_fp32_e5m2")})
         del srcs, dst
+
+    # ---- device copy 1 GiB: the practical streaming ceiling and the counters' calibration kernel -----
+    if "copy" in only:
+        n = 256 * 1024 * 1024
+        src = torch.randn(n, device=dev, generator=g)
+        dsts = [torch.empty(n, device=dev) for _ in range(2)]
+
+        def f(i=0):
+            dsts[i % 2].copy_(src)
+        ms = timed(f, max(K, 20), W)
+        nbytes = n * 4 * 2
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        secondary.append({"workload": "device copy 1 GiB FP32 (torch copy_), reference rate", "id": "copy_1gib",
+                          "value": round(gbs, 1), "unit": "GB/s", "ms_per_call": round(ms, 4), "bytes_per_call": nbytes,
+                          "roofline": roof("hbm", gbs, HBM_PEAK_GBS, "GB/s", "copy_1gib")})
+        del src, dsts
 
     # ---- CPU baseline: the oracle's FFMA chain on a slab of the 8192^3 GEMM ---------------------------
     cpu = None
@@ -251,8 +283,7 @@ def main():
         res.update({"value": round(tf, 1), "ms_per_step": round(out["gemm"]["ms"], 4),
                     "config": {"workload": "gemm 8192x8192x8192 E5M2 x E4M3 -> BF16, TN, scale_inv 1/64, alpha 1, "
                                            "beta 0 (BASELINE config 3 shape, north-star pairing)"},
-                    "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": FP8_PEAK_TFLOPS,
-                                 "unit": "TFLOP/s", "frac": round(tf / FP8_PEAK_TFLOPS, 4), "traffic": None}})
+                    "roofline": roof("mfma", tf, FP8_PEAK_TFLOPS, "TFLOP/s", "gemm_8192_e5m2xe4m3")})
     else:
         res.update({"value": None, "ms_per_step": None, "config": {"workload": "gemm not run (--only)"}})
     res["cpu_baseline"] = cpu

@@ -11,6 +11,12 @@ namespace {
 using namespace dev;
 constexpr int kThreads = 256;
 constexpr int kVec = 16;
+#ifndef E5MA_CAST_GRID
+#define E5MA_CAST_GRID 8192
+#endif
+#ifndef E5MA_CAST_NT
+#define E5MA_CAST_NT 0
+#endif
 
 template <int TI, int TO, bool VEC, bool AMAX>
 __global__ __launch_bounds__(kThreads) void cast_kernel(const void *__restrict__ src, void *__restrict__ dst,
@@ -24,9 +30,9 @@ __global__ __launch_bounds__(kThreads) void cast_kernel(const void *__restrict__
   if constexpr (VEC) {
     const size_t nvec = count / kVec;
     for (size_t c = tid; c < nvec; c += stride) {
-      Pack<TI, kVec> in;
+      Pack<TI, kVec, E5MA_CAST_NT> in;
       in.load(src, c * kVec);
-      Pack<TO, kVec> out;
+      Pack<TO, kVec, E5MA_CAST_NT> out;
       out.clear();
 #pragma unroll
       for (int e = 0; e < kVec; ++e) {
@@ -51,9 +57,8 @@ hipError_t cast_to(const void *src, void *dst, size_t count, const float *sinv, 
                    hipStream_t s) {
   const bool vec = (((uintptr_t)src | (uintptr_t)dst) & 15u) == 0;
   const size_t work = vec ? (count + kVec - 1) / kVec : count;
-  // a few resident blocks per CU keep enough dwordx4 loads in flight; more would only add amax atomics
   const size_t blocks = (work + kThreads - 1) / kThreads;
-  const int grid = (int)(blocks < 2048 ? blocks : 2048);
+  const int grid = (int)(blocks < E5MA_CAST_GRID ? blocks : E5MA_CAST_GRID);
 #define E5MA_CAST_LAUNCH(V, A) \
   cast_kernel<TI, TO, V, A><<<grid, kThreads, 0, s>>>(src, dst, count, sinv, qs, amax)
   if (vec) {

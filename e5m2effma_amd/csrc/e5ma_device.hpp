@@ -149,7 +149,10 @@ __device__ __forceinline__ void amax_commit_block(float *amax, float m, float *r
   if (threadIdx.x == 0) {
     float b = red[0];
     for (int i = 1; i < nw; ++i) b = fmaxf(b, red[i]);
-    if (b > 0.f) atomicMax((int *)amax, __float_as_int(b));
+    // With many blocks, most maxima are below the value already in *amax: skip their atomics.  The
+    // read may be stale, which only costs an atomic; the atomicMax alone decides the result.
+    if (b > 0.f && __float_as_int(b) > __atomic_load_n((const int *)amax, __ATOMIC_RELAXED))
+      atomicMax((int *)amax, __float_as_int(b));
   }
 }
 

@@ -6,8 +6,11 @@
 namespace e5ma {
 namespace dev {
 
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
 // N elements of dtype T as N * bytes(T) / 16 dwordx4 words (N * bytes(T) must be a multiple of 8).
-template <int T, int N> struct Pack {
+// NT: 16-byte accesses are non-temporal (data touched once).
+template <int T, int N, bool NT = false> struct Pack {
   static constexpr int kBytes = N * elem_bytes(T);
   static constexpr int kWords = kBytes / 4;
   uint32_t w[kWords];
@@ -17,8 +20,8 @@ template <int T, int N> struct Pack {
     if constexpr (kBytes % 16 == 0) {
 #pragma unroll
       for (int q = 0; q < kBytes / 16; ++q) {
-        const uint4 v = ((const uint4 *)p)[q];
-        w[4 * q] = v.x; w[4 * q + 1] = v.y; w[4 * q + 2] = v.z; w[4 * q + 3] = v.w;
+        const u32x4 v = NT ? __builtin_nontemporal_load((const u32x4 *)p + q) : ((const u32x4 *)p)[q];
+        w[4 * q] = v[0]; w[4 * q + 1] = v[1]; w[4 * q + 2] = v[2]; w[4 * q + 3] = v[3];
       }
     } else {
 #pragma unroll
@@ -32,7 +35,11 @@ template <int T, int N> struct Pack {
     uint8_t *p = (uint8_t *)base + i * elem_bytes(T);
     if constexpr (kBytes % 16 == 0) {
 #pragma unroll
-      for (int q = 0; q < kBytes / 16; ++q) ((uint4 *)p)[q] = make_uint4(w[4 * q], w[4 * q + 1], w[4 * q + 2], w[4 * q + 3]);
+      for (int q = 0; q < kBytes / 16; ++q) {
+        const u32x4 v{w[4 * q], w[4 * q + 1], w[4 * q + 2], w[4 * q + 3]};
+        if constexpr (NT) __builtin_nontemporal_store(v, (u32x4 *)p + q);
+        else ((u32x4 *)p)[q] = v;
+      }
     } else {
 #pragma unroll
       for (int q = 0; q < kBytes / 8; ++q) ((uint2 *)p)[q] = make_uint2(w[2 * q], w[2 * q + 1]);
