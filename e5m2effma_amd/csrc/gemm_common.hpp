@@ -6,6 +6,7 @@ namespace e5ma {
 namespace gemm {
 
 typedef int v8i __attribute__((ext_vector_type(8)));
+typedef int v2i __attribute__((ext_vector_type(2)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
@@ -111,9 +112,19 @@ __device__ __attribute__((noinline)) float epilogue_block(const dev::Epilogue &e
 
 }  // namespace gemm
 
-bool gemm_f8_tn_applies(int at, int bt, bool akc, bool bkc, int m, int n, int k);
-hipError_t launch_gemm_f8_tn(int at, int bt, const uint8_t *A, long long lda, const uint8_t *B, long long ldb, int m,
-                             int n, int k, const dev::Epilogue &e, hipStream_t s);
+// fast FP8 x FP8 path (gemm_f8.hip), any operand layout; akc / bkc: A / B K-contiguous
+bool gemm_f8_applies(int at, int bt, bool akc, bool bkc, int m, int n, int k);
+hipError_t launch_gemm_f8(int at, int bt, bool akc, bool bkc, const uint8_t *A, long long lda, const uint8_t *B,
+                          long long ldb, int m, int n, int k, const dev::Epilogue &e, hipStream_t s);
+// its instances, one translation unit per layout pair, named for (transa, transb):
+// tn = both K-contiguous, nn = A M-contiguous, nt = both M / N-contiguous, tt = B N-contiguous
+#define E5MA_F8_LAYOUT_DECL(NAME)                                                                                   \
+  hipError_t NAME(int at, int bt, const uint8_t *A, long long lda, const uint8_t *B, long long ldb, int m, int n, \
+                  int k, const dev::Epilogue &e, hipStream_t s)
+E5MA_F8_LAYOUT_DECL(launch_gemm_f8_tn);
+E5MA_F8_LAYOUT_DECL(launch_gemm_f8_nn);
+E5MA_F8_LAYOUT_DECL(launch_gemm_f8_nt);
+E5MA_F8_LAYOUT_DECL(launch_gemm_f8_tt);
 hipError_t launch_gemm_generic(int at, int bt, bool akc, bool bkc, const uint8_t *A, long long lda, const uint8_t *B,
                                long long ldb, int m, int n, int k, const dev::Epilogue &e, hipStream_t s);
 

@@ -1,0 +1,6 @@
+// gemm_f8_tt.hip -- instances of the fast FP8 GEMM for transa, transb = t, t (A K-contiguous, B N-contiguous).
+#include "gemm_f8_kernel.hpp"
+
+namespace e5ma {
+E5MA_F8_LAYOUT_DECL(launch_gemm_f8_tt) { return launch_layout<true, false>(at, bt, A, lda, B, ldb, m, n, k, e, s); }
+}  // namespace e5ma

@@ -186,3 +186,97 @@ def test_f8_path_layouts(dev, ta, tb):
     case = gu.GemmCase(rng, ta, tb, 200, 136, 8192 + 16, E5, E4, ddt=E5, qscale=0.5, amax=True, sa=0.25, sb=2.0)
     bad, first = case.run_and_check(dev)
     assert bad == 0, first
+
+
+# ---- the fast FP8 kernel in every layout (k a multiple of 256; an M / N-contiguous operand needs
+# m / n a multiple of 16): tiles of 256 x 256 with m / n tails, the transposing LDS reads of
+# M / N-contiguous operands --------------------------------------------------------------------------
+@pytest.mark.parametrize("adt,bdt", [(E5, E4), (E4, E5)])
+@pytest.mark.parametrize("ta,tb", LAYOUTS)
+def test_f8_fast_layouts(dev, ta, tb, adt, bdt):
+    rng = np.random.default_rng(ta * 4 + tb * 2 + adt + 8320)
+    case = gu.GemmCase(rng, ta, tb, 272, 304, 8192, adt, bdt, ddt=B16, pad=32)
+    bad, first = case.run_and_check(dev)
+    assert bad == 0, first
+
+
+@pytest.mark.parametrize("ta,tb", LAYOUTS)
+def test_f8_fast_layouts_full_epilogue(dev, ta, tb):
+    """OUTER scale vectors, alpha, bias and accumulation into D (beta = 1, C = NULL), FP32 output."""
+    rng = np.random.default_rng(ta * 2 + tb + 8400)
+    m, n = 288, 160
+    sa = rng.uniform(0.25, 2.0, m).astype(np.float32)
+    sb = rng.uniform(0.25, 2.0, n).astype(np.float32)
+    case = gu.GemmCase(rng, ta, tb, m, n, 8192, E5, E5, ddt=F32, alpha=0.75, sa=sa, sb=sb, biasdt=B16, beta=1.0,
+                       dist="normal", sigma=4.0)
+    bad, first = case.run_and_check(dev)
+    assert bad == 0, first
+
+
+@pytest.mark.parametrize("ta,tb", LAYOUTS)
+def test_f8_fast_layouts_fp8_output(dev, ta, tb):
+    rng = np.random.default_rng(ta * 2 + tb + 8500)
+    case = gu.GemmCase(rng, ta, tb, 256, 512, 8192, E4, E4, ddt=E5, qscale=0.5, amax=True, sa=0.25, sb=2.0,
+                       dist="normal", sigma=2.0, pad=0)
+    bad, first = case.run_and_check(dev)
+    assert bad == 0, first
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1)])
+def test_f8_fast_mn_tails_fall_back(dev, ta, tb):
+    """m not a multiple of 16 with an M-contiguous A: the general kernel takes the call."""
+    rng = np.random.default_rng(ta * 2 + tb + 8600)
+    case = gu.GemmCase(rng, ta, tb, 100, 48, 8192, E5, E4, ddt=F32)
+    bad, first = case.run_and_check(dev)
+    assert bad == 0, first
+
+
+def test_config4_dgrad_shape(dev):
+    """TE dgrad: dX = W^T dY, e5ma_gemm(N, N, in, batch, out) with W E4M3 N(0, 0.02)
+    (M-contiguous), dY E5M2 N(0, 1e-3), row-wise scale_inv vectors on both, BF16 out.  k = out = 14336
+    as in the config; m, n reduced (sampled check)."""
+    rng = np.random.default_rng(14336)
+    m, n, k = 512, 384, 14336
+    W = oracle.encode(E4, (rng.standard_normal(m * k) * 0.02 * 64).astype(np.float32))
+    dY = oracle.encode(E5, (rng.standard_normal(k * n) * 1e-3 * 1024).astype(np.float32))
+    sa = np.full(m, 1 / 64, np.float32) * rng.uniform(0.5, 2, m).astype(np.float32)
+    sb = np.full(n, 1 / 1024, np.float32) * rng.uniform(0.5, 2, n).astype(np.float32)
+    case = gu.GemmCase(None, 0, 0, m, n, k, E4, E5, ddt=B16, sa=sa, sb=sb, pad=0, A=W, B=dY)
+    s, D, _ = case.run(dev)
+    assert s == 0
+    bad, first = case.check(D, samples=4096, rng=rng)
+    assert bad == 0, first
+
+
+def test_config4_wgrad_shape(dev):
+    """TE wgrad: main_grad += dY X^T + bias, e5ma_gemm(N, T, out, in, batch, beta = 1,
+    C = NULL) with dY E5M2 (M-contiguous) and X E4M3 (N-contiguous), FP32 D.  k = batch = 8192; m, n
+    reduced (sampled check)."""
+    rng = np.random.default_rng(8192 + 4096)
+    m, n, k = 768, 512, 8192
+    dY = oracle.encode(E5, (rng.standard_normal(m * k) * 1e-3 * 1024).astype(np.float32))
+    X = oracle.encode(E4, (rng.standard_normal(k * n) * 0.5).astype(np.float32))
+    case = gu.GemmCase(rng, 0, 1, m, n, k, E5, E4, ddt=F32, sa=1 / 1024, sb=1.0, beta=1.0, biasdt=F32, pad=0,
+                       A=dY, B=X, D0=rng.uniform(-1, 1, (m + 3) * n).astype(np.float32))
+    s, D, _ = case.run(dev)
+    assert s == 0
+    bad, first = case.check(D, samples=4096, rng=rng)
+    assert bad == 0, first
+
+
+def test_config4_e5m2_output_inf_nan(dev):
+    """Config 4 run 3: dgrad layout with E5M2 output, scale and amax, and about 0.001 % of dY set to the
+    E5M2 Inf / NaN codes: those columns saturate / become NaN, amax (NaN ignored) becomes Inf."""
+    rng = np.random.default_rng(3)
+    m, n, k = 256, 256, 8192
+    W = oracle.encode(E4, (rng.standard_normal(m * k) * 0.02 * 64).astype(np.float32))
+    dY = oracle.encode(E5, (rng.standard_normal(k * n) * 1e-3 * 1024).astype(np.float32))
+    hit = rng.choice(k * n, max(2, k * n // 100000), replace=False)
+    dY[hit] = rng.choice(np.array([0x7C, 0xFC, 0x7D, 0x7E, 0x7F, 0xFF], np.uint8), hit.size)
+    case = gu.GemmCase(None, 0, 0, m, n, k, E4, E5, ddt=E5, sa=1 / 64, sb=1 / 1024, qscale=4.0, amax=True, pad=0,
+                       A=W, B=dY)
+    s, D, amax = case.run(dev)
+    assert s == 0
+    bad, first = case.check(D, samples=4096, rng=rng)
+    assert bad == 0, first
+    assert amax == np.inf
