@@ -3,7 +3,8 @@
 Headline ("step" = one e5ma_gemm call): the 8192^3 E5M2 x E4M3 -> BF16 GEMM (TN, per-tensor
 scale_inv 1/64, inputs N(0,1)*8 with 0.01 % set to the largest finite value), reported in TFLOP/s and as
 a fraction of the FP8 dense matrix-core peak.  Secondary lines (same JSON object, "secondary"): the
-same GEMM with E5M2 x E5M2 and E5M2 x BF16 operands, GEMV 8192 x 8192 at batch 1 and 8 (weights rotated
+same GEMM with E5M2 x E5M2 and E5M2 x BF16 operands, the three TE backward GEMMs of config 4 (dgrad,
+wgrad into an FP32 main_grad, dgrad with E5M2 output), GEMV 8192 x 8192 at batch 1 and 8 (weights rotated
 through 6 distinct buffers so the 256 MB Infinity Cache cannot serve them), the fused AdamW step over
 256M parameters (BF16 and FP32 state, E5M2 copy) and the 8192^2 FP32 -> E5M2 cast.
 
@@ -16,7 +17,7 @@ calibration; null where no counter run covers the workload.  cpu_baseline: the o
 FFMA-chain GEMM (oracle/e5ma_oracle.c, the reference's host emulation order) timed on this host on a
 slab of output rows and scaled to the full problem.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only gemm,gemv,adam,cast,copy] [--no-cpu]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only gemm,te,gemv,adam,cast,copy] [--no-cpu]
 """
 import argparse
 import ctypes
@@ -48,8 +49,8 @@ def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=20)
-    p.add_argument("--warmup", type=int, default=5)
-    p.add_argument("--only", default="gemm,gemv,adam,cast,copy")
+    p.add_argument("--warmup", type=int, default=30)  # the clock under FP8 matrix load settles in ~20 ms
+    p.add_argument("--only", default="gemm,te,gemv,adam,cast,copy")
     p.add_argument("--no-cpu", action="store_true")
     return p.parse_args()
 
@@ -147,6 +148,58 @@ def main():
                               "value": round(t2, 1), "unit": "TFLOP/s", "ms_per_call": round(ms2, 4),
                               "roofline": roof("mfma", t2, peak, "TFLOP/s", f"gemm_8192_{name.lower()}")})
         del A8, B8, Bbf, D
+
+    # ---- config 4: TE HYBRID backward GEMMs, tokens 8192, hidden 4096, ffn 14336 ----------------------
+    if "te" in only:
+        tok, hid, ffn = 8192, 4096, 14336
+        g.manual_seed(0xE5A004 + 1)
+        Wq = quantize(torch.randn(ffn * hid, device=dev, generator=g) * (0.02 * 64), E4M3)  # [ffn, hid] row-major
+        dY = quantize(torch.randn(tok * ffn, device=dev, generator=g) * (1e-3 * 1024), E5M2)  # [tok, ffn] row-major
+        X = quantize(torch.randn(tok * hid, device=dev, generator=g) * 2.0, E4M3)            # [tok, hid] row-major
+        sw = torch.full((hid,), 1 / 64, device=dev)     # row-wise scale_inv of W^T (m = hid)
+        sdy = torch.full((tok,), 1 / 1024, device=dev)  # row-wise scale_inv of dY (n = tok)
+        dX = torch.empty(hid * tok, dtype=torch.bfloat16, device=dev)
+        G = torch.zeros(ffn * hid, dtype=torch.float32, device=dev)
+        bias = torch.zeros(ffn, dtype=torch.float32, device=dev)
+        dX8 = torch.empty(hid * tok, dtype=torch.uint8, device=dev)
+        am = torch.zeros(1, dtype=torch.float32, device=dev)
+        dY_bad = dY.clone()
+        hit = torch.randint(0, dY_bad.numel(), (dY_bad.numel() // 100000,), device=dev, generator=g)
+        dY_bad[hit] = 0x7E  # E5M2 NaN codes (0.001 %)
+        Wt = _lib.tensor(Wq.data_ptr(), E4M3, sw.data_ptr(), None, None, 1)
+        dYt = _lib.tensor(dY.data_ptr(), E5M2, sdy.data_ptr(), None, None, 1)
+        dYb = _lib.tensor(dY_bad.data_ptr(), E5M2, sdy.data_ptr(), None, None, 1)
+        dYw = _lib.tensor(dY.data_ptr(), E5M2, f32(1 / 1024))
+        Xt = _lib.tensor(X.data_ptr(), E4M3, f32(0.5))
+        dXt = _lib.tensor(dX.data_ptr(), BF16)
+        dX8t = _lib.tensor(dX8.data_ptr(), E5M2, None, f32(4.0), am.data_ptr())
+        Gt = _lib.tensor(G.data_ptr(), FP32)
+        Bt = _lib.tensor(bias.data_ptr(), FP32)
+
+        # dgrad: dX^T [hid, tok] = W^T dY^T, column-major: e5ma_gemm(N, N, hid, tok, ffn), A = W (lda = hid),
+        # B = dY (ldb = ffn), OUTER scale_inv vectors on both
+        def dgrad(i=0, Bd=dYt, Dd=dXt):
+            check(L.e5ma_gemm(0, 0, hid, tok, ffn, 1.0, ctypes.byref(Wt), hid, ctypes.byref(Bd), ffn, 0.0, None, 0,
+                              ctypes.byref(Dd), hid, None, sp), "dgrad")
+
+        # wgrad: main_grad [ffn, hid] (column-major ffn x hid) += dY^T X + bias: e5ma_gemm(N, T, ffn, hid, tok),
+        # A = dY (lda = ffn), B = X (ldb = hid), beta = 1, C = NULL
+        def wgrad(i=0):
+            check(L.e5ma_gemm(0, 1, ffn, hid, tok, 1.0, ctypes.byref(dYw), ffn, ctypes.byref(Xt), hid, 1.0, None, 0,
+                              ctypes.byref(Gt), ffn, ctypes.byref(Bt), sp), "wgrad")
+
+        def dgrad8(i=0):
+            dgrad(i, dYb, dX8t)
+        flop = 2.0 * hid * tok * ffn
+        for name, wid, fn in (("dgrad (N,N) E4M3 W x E5M2 dY, row-wise scale_inv, BF16 out", "te_dgrad", dgrad),
+                              ("wgrad (N,T) E5M2 dY x E4M3 X, beta=1 into FP32 main_grad + bias", "te_wgrad", wgrad),
+                              ("dgrad (N,N) E5M2 out, scale + amax, 0.001% NaN codes in dY", "te_dgrad_e5m2", dgrad8)):
+            ms = timed(fn, max(3, K // 2), max(W, 3))
+            tf = flop / (ms * 1e-3) / 1e12
+            secondary.append({"workload": f"TE config 4 {name}", "id": wid, "value": round(tf, 1), "unit": "TFLOP/s",
+                              "ms_per_call": round(ms, 4),
+                              "roofline": roof("mfma", tf, FP8_PEAK_TFLOPS, "TFLOP/s", wid)})
+        del Wq, dY, X, dX, G, dX8, dY_bad
 
     # ---- GEMV 8192^2, batch 1 and 8 -----------------------------------------------------------------
     if "gemv" in only:
