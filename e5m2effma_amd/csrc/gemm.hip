@@ -8,6 +8,7 @@ hipError_t launch_gemm(int at, int bt, bool akc, bool bkc, const uint8_t *A, lon
                        long long ldb, int m, int n, int k, const dev::Epilogue &e, const DeviceInfo &,
                        hipStream_t s) {
   if (gemm_f8_applies(at, bt, akc, bkc, m, n, k)) return launch_gemm_f8(at, bt, akc, bkc, A, lda, B, ldb, m, n, k, e, s);
+  if (gemm_h_applies(at, bt, akc, bkc, m, n, k)) return launch_gemm_h(at, bt, akc, bkc, A, lda, B, ldb, m, n, k, e, s);
   return launch_gemm_generic(at, bt, akc, bkc, A, lda, B, ldb, m, n, k, e, s);
 }
 

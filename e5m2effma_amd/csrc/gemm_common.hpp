@@ -125,6 +125,16 @@ E5MA_F8_LAYOUT_DECL(launch_gemm_f8_tn);
 E5MA_F8_LAYOUT_DECL(launch_gemm_f8_nn);
 E5MA_F8_LAYOUT_DECL(launch_gemm_f8_nt);
 E5MA_F8_LAYOUT_DECL(launch_gemm_f8_tt);
+// fast BF16-matrix-core path (gemm_h.hip): FP8 A x FP8 B (k < kF8MinK) or x K-contiguous BF16 B
+bool gemm_h_applies(int at, int bt, bool akc, bool bkc, int m, int n, int k);
+hipError_t launch_gemm_h(int at, int bt, bool akc, bool bkc, const uint8_t *A, long long lda, const uint8_t *B,
+                         long long ldb, int m, int n, int k, const dev::Epilogue &e, hipStream_t s);
+E5MA_F8_LAYOUT_DECL(launch_gemm_h_tn);
+E5MA_F8_LAYOUT_DECL(launch_gemm_h_nn);
+E5MA_F8_LAYOUT_DECL(launch_gemm_h_nt);
+E5MA_F8_LAYOUT_DECL(launch_gemm_h_tt);
+E5MA_F8_LAYOUT_DECL(launch_gemm_h_tn_bf16);
+E5MA_F8_LAYOUT_DECL(launch_gemm_h_nn_bf16);
 hipError_t launch_gemm_generic(int at, int bt, bool akc, bool bkc, const uint8_t *A, long long lda, const uint8_t *B,
                                long long ldb, int m, int n, int k, const dev::Epilogue &e, hipStream_t s);
 

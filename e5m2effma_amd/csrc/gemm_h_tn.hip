@@ -1,0 +1,6 @@
+// gemm_h_tn.hip -- instances of the BF16-matrix-core GEMM for transa, transb = t, n (A K-contiguous, B K-contiguous).
+#include "gemm_h_kernel.hpp"
+
+namespace e5ma {
+E5MA_F8_LAYOUT_DECL(launch_gemm_h_tn) { return hk::launch_layout<true, true>(at, bt, A, lda, B, ldb, m, n, k, e, s); }
+}  // namespace e5ma

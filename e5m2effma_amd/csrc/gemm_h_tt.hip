@@ -1,0 +1,6 @@
+// gemm_h_tt.hip -- instances of the BF16-matrix-core GEMM for transa, transb = t, t (A K-contiguous, B N-contiguous).
+#include "gemm_h_kernel.hpp"
+
+namespace e5ma {
+E5MA_F8_LAYOUT_DECL(launch_gemm_h_tt) { return hk::launch_layout<true, false>(at, bt, A, lda, B, ldb, m, n, k, e, s); }
+}  // namespace e5ma

@@ -280,3 +280,74 @@ def test_config4_e5m2_output_inf_nan(dev):
     bad, first = case.check(D, samples=4096, rng=rng)
     assert bad == 0, first
     assert amax == np.inf
+
+
+# ---- the BF16-matrix-core kernel: FP8 x FP8 with k < 8192 (k a multiple of 256) in every layout, and
+# FP8 x K-contiguous BF16 (k a multiple of 128); FP8 widened exactly to BF16 per MFMA step ----------
+@pytest.mark.parametrize("adt,bdt", [(E5, E4), (E4, E5), (E5, E5)])
+@pytest.mark.parametrize("ta,tb", LAYOUTS)
+def test_h_fast_fp8_layouts(dev, ta, tb, adt, bdt):
+    rng = np.random.default_rng(ta * 4 + tb * 2 + adt * 7 + bdt + 9100)
+    case = gu.GemmCase(rng, ta, tb, 272, 304, 1024, adt, bdt, ddt=B16, pad=32)
+    bad, first = case.run_and_check(dev)
+    assert bad == 0, first
+
+
+@pytest.mark.parametrize("adt", [E5, E4])
+@pytest.mark.parametrize("ta", [1, 0])
+@pytest.mark.parametrize("k", [256, 2048])
+def test_h_fast_fp8_x_bf16(dev, ta, adt, k):
+    rng = np.random.default_rng(ta * 2 + adt * 3 + k + 9200)
+    case = gu.GemmCase(rng, ta, 0, 336, 272, k, adt, B16, ddt=B16, pad=16, dist="normal", sigma=3.0)
+    bad, first = case.run_and_check(dev)
+    assert bad == 0, first
+
+
+@pytest.mark.parametrize("ta,tb,bdt", [(1, 0, B16), (0, 0, B16), (0, 1, E4), (1, 1, E5)])
+def test_h_fast_full_epilogue(dev, ta, tb, bdt):
+    """OUTER scale vectors (FP8 operands), alpha, bias, beta * C of another dtype, FP32 output."""
+    rng = np.random.default_rng(ta * 2 + tb + bdt + 9300)
+    m, n = 288, 160
+    sa = rng.uniform(0.25, 2.0, m).astype(np.float32)
+    sb = rng.uniform(0.25, 2.0, n).astype(np.float32) if bdt != B16 else 0.5
+    case = gu.GemmCase(rng, ta, tb, m, n, 512, E4, bdt, ddt=F32, alpha=0.75, sa=sa, sb=sb, biasdt=F16, beta=0.5,
+                       cdt=B16)
+    bad, first = case.run_and_check(dev)
+    assert bad == 0, first
+
+
+@pytest.mark.parametrize("ta,tb,bdt", [(1, 0, B16), (0, 0, E5), (0, 1, E4)])
+def test_h_fast_fp8_output(dev, ta, tb, bdt):
+    rng = np.random.default_rng(ta * 2 + tb + bdt + 9400)
+    case = gu.GemmCase(rng, ta, tb, 256, 512, 1024, E5, bdt, ddt=E4, qscale=0.25, amax=True, sa=0.5, pad=0,
+                       dist="normal", sigma=2.0)
+    bad, first = case.run_and_check(dev)
+    assert bad == 0, first
+
+
+def test_h_fast_inf_nan_operands(dev):
+    """E5M2 Inf / NaN codes widen to BF16 Inf / NaN: saturated / NaN outputs and an Inf amax."""
+    rng = np.random.default_rng(9500)
+    m, n, k = 256, 256, 512
+    case = gu.GemmCase(rng, 1, 0, m, n, k, E5, B16, ddt=E5, qscale=1.0, amax=True, pad=0, dist="normal", sigma=0.5)
+    A = case.A.copy()
+    A[3 * k + 5] = 0x7C   # +Inf in row 3
+    A[77 * k + 9] = 0xFC  # -Inf in row 77
+    A[150 * k + 1] = 0x7E  # NaN in row 150
+    case.A = A
+    s, D, amax = case.run(dev)
+    assert s == 0
+    bad, first = case.check(D)
+    assert bad == 0, first
+    assert amax == np.inf
+
+
+def test_h_config3_fp8_x_bf16_sampled(dev):
+    """Config 3's second GEMM (E5M2 A x BF16 B, N(0,1) * 8 values, scale_inv 1/64 on A) at k = 8192 on a
+    2048 x 2048 output, sampled check."""
+    rng = np.random.default_rng(9600)
+    case = gu.GemmCase(rng, 1, 0, 2048, 2048, 8192, E5, B16, ddt=B16, dist="normal", sigma=8.0, sa=1 / 64, pad=0)
+    s, D, _ = case.run(dev)
+    assert s == 0
+    bad, first = case.check(D, samples=4096, rng=rng)
+    assert bad == 0, first
