@@ -100,31 +100,38 @@ template <bool KC> __device__ __forceinline__ v8i read_frag(const uint8_t *s, in
   }
 }
 
-// Stage s (= SLOT mod 4) of the K loop; a / b hold stage s's fragments.  WAITN: global loads this
-// wave may leave in flight when stage s + 1 must have landed; NEXT: a stage s + 1 exists; ISSUE:
-// stage s + 4 exists.  After the barrier the 16 MFMAs of stage s are issued; the loads of stage s + 4
-// into stage s's slot (free: every wave read it before the barrier) go out one pair after every
-// fourth MFMA, and each fragment register is refilled from stage s + 1 right after its last use, with
-// the LDS reads spread one per MFMA.  (Issuing the 8 loads as one burst stalled the MFMA stream.)
+// Stage s (= SLOT mod 4) of the K loop.  The fragments are double-buffered by stage parity: set
+// P = SLOT & 1 holds stage s's, and stage s + 1's are read into set 1 - P from the start of stage s, one
+// fragment every second MFMA (LDS reads interleaved one per MFMA), so they have the whole stage to
+// land.  (Single-buffered, the last reads of a stage were issued with its last MFMAs; slowed by the
+// direct-to-LDS writes, they left the matrix cores idle at the barrier.)  WAITN: global loads this wave
+// may leave in flight when stage s + 1 must have landed; NEXT: a stage s + 1 exists; ISSUE: stage s + 4
+// exists.  The loads of stage s + 4 into stage s's slot (free: every wave read it before the barrier)
+// go out one pair after every fourth MFMA.  (Issuing the 8 loads as one burst stalled the MFMA stream.)
 template <int WAITN, bool NEXT, bool ISSUE, int SLOT, int AT, int BT, bool AKC, bool BKC>
 __device__ __forceinline__ void f8_stage(const TileArgs &t, int s, int i0, int j0, int wave, int lane, int wm, int wn,
-                                         v8i (&a)[4], v8i (&b)[4], v16f (&acc)[4][4]) {
+                                         v8i (&a)[2][4], v8i (&b)[2][4], v16f (&acc)[4][4]) {
+  constexpr int P = SLOT & 1, Q = P ^ 1;
   if constexpr (NEXT) wait_barrier<WAITN>();
   const uint8_t *na = lds_a<(SLOT + 1) & 3>(), *nb = lds_b<(SLOT + 1) & 3>();
 #pragma unroll
   for (int x = 0; x < 4; ++x) {
 #pragma unroll
     for (int y = 0; y < 4; ++y) {
-      acc[x][y] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a[x], b[y], acc[x][y], kMfmaFmt<AT>, kMfmaFmt<BT>, 0,
-                                                                  kNeutralScale, 0, kNeutralScale);
+      acc[x][y] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a[P][x], b[P][y], acc[x][y], kMfmaFmt<AT>,
+                                                                  kMfmaFmt<BT>, 0, kNeutralScale, 0, kNeutralScale);
       if constexpr (ISSUE) {
         if (y == 1) issue_load<SLOT, AKC, BKC>(t, (s + 4) * kBK, i0, j0, wave, lane, x);
       }
       if constexpr (NEXT) {
-        if (x == 3) b[y] = read_frag<BKC>(nb, 128 * wn + 32 * y, lane);
+        const int i = 4 * x + y;  // fragment i / 2 of the next stage after MFMA i (i even)
+        if ((i & 1) == 0) {
+          const int f = i >> 1;
+          if (f < 4) a[Q][f] = read_frag<AKC>(na, 128 * wm + 32 * f, lane);
+          else b[Q][f - 4] = read_frag<BKC>(nb, 128 * wn + 32 * (f - 4), lane);
+        }
       }
     }
-    if constexpr (NEXT) a[x] = read_frag<AKC>(na, 128 * wm + 32 * x, lane);
   }
   if constexpr (NEXT) {
     // keep the LDS reads spread over the MFMA stream: MFMA, DS read, MFMA, DS read, ...
@@ -160,11 +167,11 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_f8_kernel(TileArgs t, Epilog
   issue_stage<2, AKC, BKC>(t, 2 * kBK, i0, j0, wave, lane);
   wait_barrier<2 * 2 * kLoadsPerWave>();  // stage 0 landed; stages 1 and 2 may be in flight
   issue_stage<3, AKC, BKC>(t, 3 * kBK, i0, j0, wave, lane);
-  v8i a[4], b[4];
+  v8i a[2][4], b[2][4];  // fragments, double-buffered by stage parity
 #pragma unroll
   for (int x = 0; x < 4; ++x) {
-    a[x] = read_frag<AKC>(lds_a<0>(), 128 * wm + 32 * x, lane);
-    b[x] = read_frag<BKC>(lds_b<0>(), 128 * wn + 32 * x, lane);
+    a[0][x] = read_frag<AKC>(lds_a<0>(), 128 * wm + 32 * x, lane);
+    b[0][x] = read_frag<BKC>(lds_b<0>(), 128 * wn + 32 * x, lane);
   }
   // steady state, four stages (one per ring slot) per iteration: stages s + 2 and s + 3 in flight
   // while s + 1 is awaited; then the last four stages drain the ring (nk % 4 == 0)
