@@ -305,6 +305,12 @@ __global__ __launch_bounds__(kThreads) void gemv_dot_kernel(const uint8_t *A, lo
 
 // ---- x staged in LDS by direct-to-LDS loads (n <= 2, k * n * bytes(x) <= kXLds) ----------------
 constexpr int kXLds = 32768;
+#ifndef E5MA_GEMV_RX
+#define E5MA_GEMV_RX 2  // rows per wave
+#endif
+#ifndef E5MA_GEMV_UX
+#define E5MA_GEMV_UX 4  // 16-byte chunks per lane and row in flight
+#endif
 typedef __attribute__((address_space(3))) void lds_void_t;
 
 // one direct-to-LDS load: 16 bytes per lane from src to lds + 16 * lane (lds wave-uniform); inline asm,
@@ -331,13 +337,18 @@ template <int BT> __device__ __forceinline__ void xlds_pairs(const uint8_t *xs, 
 // As gemv_dot_kernel, but the block first copies x into LDS with direct-to-LDS loads (issued before
 // the weight loads, so they complete first), then waits only for those, so x never occupies the
 // vector-memory pipe again and the weights stream alone.
-// 256-thread blocks, 2 rows and 4 chunks per lane and batch (measured best of 1 / 2 / 4 rows, 4 / 8
-// chunks and 256 / 1024-thread blocks on the 8192 x 8192 batch-1 shape)
-constexpr int kXThreads = 256, kXWaves = kXThreads / 64;
+// 512-thread blocks, 2 rows and 4 chunks per lane and batch (measured best of 1 / 2 / 4 rows, 4 / 8
+// chunks and 256 / 512 / 1024-thread blocks on the 8192 x 8192 batch-1 and -2 shapes: 512 threads halve
+// the x copies of 256 (13.1 vs 13.7 us at n = 1); 8 chunks need 140 VGPRs, too many for the grid's
+// 4 waves per SIMD)
+#ifndef E5MA_GEMV_XTHREADS
+#define E5MA_GEMV_XTHREADS 512
+#endif
+constexpr int kXThreads = E5MA_GEMV_XTHREADS, kXWaves = kXThreads / 64;
 template <int AT, int BT, int NB, int R, int U>
 __global__ __launch_bounds__(kXThreads) void gemv_xlds_kernel(const uint8_t *A, long long lda, const uint8_t *B,
                                                              long long ldb, int m, int k, Epilogue e) {
-  __shared__ __attribute__((aligned(1024))) uint8_t xs[kXLds];
+  extern __shared__ __attribute__((aligned(1024))) uint8_t xs[];  // x, rounded up to whole KiB
   __shared__ float red[kXWaves];
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int row0 = (blockIdx.x * kXWaves + wave) * R;
@@ -346,8 +357,8 @@ __global__ __launch_bounds__(kXThreads) void gemv_xlds_kernel(const uint8_t *A, 
   GemvOut<NB> out;
   out.fetch(e, st, row0, m, R, lane);
   const int colbytes = k * elem_bytes(BT), xtotal = colbytes * NB;
-  // x: 1 KiB per wave and step; source offsets past the end are clamped (the bytes they land on are
-  // never read)
+  // x: 1 KiB per wave and step into the dynamic LDS of round_up(xtotal, 1 KiB); source offsets past
+  // the end are clamped (the bytes they land on are never read)
   constexpr int kSteps = kXLds / (1024 * kXWaves);
 #pragma unroll
   for (int q = 0; q < kSteps; ++q) {
@@ -429,10 +440,12 @@ hipError_t gemv_n(const uint8_t *A, long long lda, const uint8_t *B, long long l
   if constexpr (BT != E5MA_FP32 && NB <= 2) {
     constexpr int R = E5MA_GEMV_R_NARROW, U = E5MA_GEMV_U_NARROW;
     const int grid = (m + kWaves * R - 1) / (kWaves * R);
-    if ((long long)k * NB * elem_bytes(BT) <= kXLds) {
-      constexpr int RX = 2, UX = 4;
+    const long long xbytes = (long long)k * NB * elem_bytes(BT);
+    if (xbytes <= kXLds) {
+      constexpr int RX = E5MA_GEMV_RX, UX = E5MA_GEMV_UX;
       const int gx = (m + kXWaves * RX - 1) / (kXWaves * RX);
-      gemv_xlds_kernel<AT, BT, NB, RX, UX><<<gx, kXThreads, 0, s>>>(A, lda, B, ldb, m, k, e);
+      const size_t lds = (size_t)((xbytes + 1023) / 1024 * 1024);
+      gemv_xlds_kernel<AT, BT, NB, RX, UX><<<gx, kXThreads, lds, s>>>(A, lda, B, ldb, m, k, e);
     } else
       gemv_dot_kernel<AT, BT, NB, R, U><<<grid, kThreads, 0, s>>>(A, lda, B, ldb, m, k, e);
   } else {  // FP32 x is not a BF16 value, and for wider x the FP32 FMA kernel measured faster
