@@ -147,6 +147,23 @@ def main():
             secondary.append({"workload": f"gemm 8192^3 {name}->BF16 TN", "id": f"gemm_8192_{name.lower()}",
                               "value": round(t2, 1), "unit": "TFLOP/s", "ms_per_call": round(ms2, 4),
                               "roofline": roof("mfma", t2, peak, "TFLOP/s", f"gemm_8192_{name.lower()}")})
+
+        # the other three layouts of the headline GEMM (the same bytes read as M / N-contiguous operands)
+        def layout_fn(ta, tb):
+            At = _lib.tensor(A8.data_ptr(), E5M2, sinv)
+            Bt = _lib.tensor(B8[E4M3].data_ptr(), E4M3, sinv)
+            Dt = _lib.tensor(D.data_ptr(), BF16)
+
+            def f(i=0):
+                check(L.e5ma_gemm(ta, tb, M, N, Kd, 1.0, ctypes.byref(At), Kd if ta else M, ctypes.byref(Bt),
+                                  N if tb else Kd, 0.0, None, 0, ctypes.byref(Dt), M, None, sp), "gemm")
+            return f
+        for ta, tb, lname in ((0, 0, "NN"), (0, 1, "NT"), (1, 1, "TT")):
+            ms2 = timed(layout_fn(ta, tb), max(3, K // 2), 2)
+            t2 = flop / (ms2 * 1e-3) / 1e12
+            secondary.append({"workload": f"gemm 8192^3 E5M2xE4M3->BF16 {lname}", "id": f"gemm_8192_{lname.lower()}",
+                              "value": round(t2, 1), "unit": "TFLOP/s", "ms_per_call": round(ms2, 4),
+                              "roofline": roof("mfma", t2, FP8_PEAK_TFLOPS, "TFLOP/s", f"gemm_8192_{lname.lower()}")})
         del A8, B8, Bbf, D
 
     # ---- config 4: TE HYBRID backward GEMMs, tokens 8192, hidden 4096, ffn 14336 ----------------------
@@ -190,16 +207,30 @@ def main():
 
         def dgrad8(i=0):
             dgrad(i, dYb, dX8t)
+
+        # wgrad from token-contiguous FP8 copies (TE's transposed caches): main_grad^T [hid, ffn] += X^T dY,
+        # e5ma_gemm(T, N, hid, ffn, tok), A = X^T storage [hid][tok], B = dY^T storage [ffn][tok]; the
+        # bytes of X and dY stand in for the transposed copies (the kernel time does not depend on values)
+        Gt2 = _lib.tensor(G.data_ptr(), FP32)
+        bias2 = torch.zeros(hid, dtype=torch.float32, device=dev)
+        Bt2 = _lib.tensor(bias2.data_ptr(), FP32)
+        Xw = _lib.tensor(X.data_ptr(), E4M3, f32(0.5))
+
+        def wgrad_tn(i=0):
+            check(L.e5ma_gemm(1, 0, hid, ffn, tok, 1.0, ctypes.byref(Xw), tok, ctypes.byref(dYw), tok, 1.0, None, 0,
+                              ctypes.byref(Gt2), hid, ctypes.byref(Bt2), sp), "wgrad_tn")
         flop = 2.0 * hid * tok * ffn
         for name, wid, fn in (("dgrad (N,N) E4M3 W x E5M2 dY, row-wise scale_inv, BF16 out", "te_dgrad", dgrad),
                               ("wgrad (N,T) E5M2 dY x E4M3 X, beta=1 into FP32 main_grad + bias", "te_wgrad", wgrad),
+                              ("wgrad (T,N) from token-contiguous copies, beta=1 into FP32 + bias", "te_wgrad_tn",
+                               wgrad_tn),
                               ("dgrad (N,N) E5M2 out, scale + amax, 0.001% NaN codes in dY", "te_dgrad_e5m2", dgrad8)):
             ms = timed(fn, max(3, K // 2), max(W, 3))
             tf = flop / (ms * 1e-3) / 1e12
             secondary.append({"workload": f"TE config 4 {name}", "id": wid, "value": round(tf, 1), "unit": "TFLOP/s",
                               "ms_per_call": round(ms, 4),
                               "roofline": roof("mfma", tf, FP8_PEAK_TFLOPS, "TFLOP/s", wid)})
-        del Wq, dY, X, dX, G, dX8, dY_bad
+        del Wq, dY, X, dX, G, dX8, dY_bad, bias2
 
     # ---- GEMV 8192^2, batch 1 and 8 -----------------------------------------------------------------
     if "gemv" in only:

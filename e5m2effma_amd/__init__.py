@@ -7,7 +7,13 @@ functional interface of the reference's Python package (reference
 * ``matmul(a, b, ...)``: ``out = alpha * (scale_a * scale_b) * (a @ b) + bias + beta * out``;
 * ``linear(x, weight, bias, ...)``: ``x @ weight.t() + bias``;
 * ``cast(x, dtype, ...)``: element-wise conversion with scale_inv / scale / amax;
-* ``adam_step(param, grad, exp_avg, exp_avg_sq, ...)``: one fused in-place Adam / AdamW step.
+* ``adam_step(param, grad, exp_avg, exp_avg_sq, ...)``: one fused in-place Adam / AdamW step;
+* ``AdamW``: a ``torch.optim`` optimizer on that step (``optim.py``);
+* ``Float8Tensor`` / ``quantize_linear_``: FP8 weights with their scale that ``@``, ``F.linear`` and
+  ``nn.Linear`` multiply on this library (``tensor.py``).
+
+On import, ``torch.e5m2effma`` (like ``e5m2``) becomes an alias of ``torch.float8_e5m2``, as with the
+reference package.
 
 Tensors live on a ROCm device; FP8 tensors use ``torch.float8_e5m2`` / ``torch.float8_e4m3fn`` (OCP,
 the encodings of this library).  Scales follow Transformer Engine: ``scale_a`` / ``scale_b`` /
@@ -27,7 +33,10 @@ from ._lib import BF16, E4M3, E5M2, FP16, FP32
 __version__ = "0.2.0"
 e5m2 = torch.float8_e5m2
 e4m3 = torch.float8_e4m3fn
-__all__ = ["matmul", "linear", "cast", "adam_step", "gemm_raw", "e5m2", "e4m3", "__version__"]
+if not hasattr(torch, "e5m2effma"):
+    torch.e5m2effma = e5m2
+__all__ = ["matmul", "linear", "cast", "adam_step", "AdamW", "Float8Tensor", "quantize_linear_", "gemm_raw", "e5m2",
+           "e4m3", "__version__"]
 
 _CODE = {torch.float8_e4m3fn: E4M3, torch.bfloat16: BF16, torch.float16: FP16, torch.float32: FP32,
          torch.float8_e5m2: E5M2}
@@ -312,3 +321,7 @@ def gemm_raw(transa, transb, m, n, k, alpha, A, lda, B, ldb, beta, C, ldc, D, ld
     st = _stream() if stream is None else ctypes.c_void_p(stream)
     return _lib.lib().e5ma_gemm(transa, transb, m, n, k, float(alpha), _lib.ref(A), lda, _lib.ref(B), ldb,
                                 float(beta), _lib.ref(C), ldc, _lib.ref(D), ldd, _lib.ref(bias), st)
+
+
+from .optim import AdamW  # noqa: E402  (they call the functions above)
+from .tensor import Float8Tensor, quantize_linear_  # noqa: E402
