@@ -47,6 +47,20 @@ const DeviceInfo &device_info(int dev) {
     snprintf(d.arch, sizeof d.arch, "%s", p.gcnArchName);
     d.supported = strncmp(p.gcnArchName, "gfx950", 6) == 0;
     d.xcds = 8;
+    if (d.supported) {
+      hipMemPoolProps props{};
+      props.allocType = hipMemAllocationTypePinned;
+      props.location.type = hipMemLocationTypeDevice;
+      props.location.id = dev;
+      hipMemPool_t pool = nullptr;
+      if (hipMemPoolCreate(&pool, &props) == hipSuccess) {
+        uint64_t keep = UINT64_MAX;
+        (void)hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep);
+        d.pool = pool;
+      } else {
+        (void)hipGetLastError();
+      }
+    }
   });
   return d;
 }

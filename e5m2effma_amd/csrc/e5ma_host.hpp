@@ -19,6 +19,10 @@ struct DeviceInfo {
   int xcds = 8;         // accelerator complex dies (L2 domains)
   bool supported = false;
   char arch[64] = {0};
+  // The library's own stream-ordered memory pool on this device (null if unavailable): split-K
+  // workspaces come from it.  Its release threshold is unlimited, so a freed workspace stays mapped
+  // and the next call reuses it, and the process's default pool keeps its own settings.
+  hipMemPool_t pool = nullptr;
 };
 // Current device's properties (cached per device); check_device() reports an unsupported device.
 const DeviceInfo &device_info(int dev);

@@ -148,8 +148,9 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_f8_kernel(TileArgs t, Epilog
   __shared__ float red[kThreads / 64];
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
-  int tm, tn;
-  tile_of(blockIdx.x, t.tiles_m, t.tiles_n, tm, tn);
+  int tm, tn, sp;
+  tile_of(blockIdx.x, t, tm, tn, sp);
+  apply_split(t, e, sp);
   const int i0 = tm * kBM, j0 = tn * kBN;
   const int nk = t.k / kBK;
 
@@ -194,7 +195,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_f8_kernel(TileArgs t, Epilog
 
 template <int AT, int BT, bool AKC, bool BKC>
 hipError_t run_d(const TileArgs &t, const Epilogue &e, hipStream_t s) {
-  const int grid = t.tiles_m * t.tiles_n;
+  const int grid = t.tiles_m * t.tiles_n * t.splits;
   // the direct epilogue needs 4-element-aligned D columns and, with OUTER scaling of A, a 16-byte
   // aligned scale vector
   const int vec = ((uintptr_t)e.d % (4 * elem_bytes(e.d_dtype))) == 0 && e.ldd % 4 == 0 &&
@@ -212,13 +213,15 @@ hipError_t run_d(const TileArgs &t, const Epilogue &e, hipStream_t s) {
   return hipGetLastError();
 }
 
-// every FP8 pairing for one layout pair
+// every FP8 pairing for one layout pair; with splits > 1, k is split into equal parts and e describes
+// the FP32 partial output of split 0 (the next split's follows at e.ldd * n floats)
 template <bool AKC, bool BKC>
 hipError_t launch_layout(int at, int bt, const uint8_t *A, long long lda, const uint8_t *B, long long ldb, int m, int n,
-                         int k, const Epilogue &e, hipStream_t s) {
-  TileArgs t{A, B, lda, ldb, m, n, k, (m + kBM - 1) / kBM, (n + kBN - 1) / kBN};
-  if (at == E5MA_E5M2)
-    return bt == E5MA_E5M2 ? run_d<E5MA_E5M2, E5MA_E5M2, AKC, BKC>(t, e, s) : run_d<E5MA_E5M2, E5MA_E4M3, AKC, BKC>(t, e, s);
+                         int k, int splits, const Epilogue &e, hipStream_t s) {
+  const int ks = k / splits;
+  TileArgs t{A, B, lda, ldb, m, n, ks, (m + kBM - 1) / kBM, (n + kBN - 1) / kBN, splits,
+             AKC ? ks : ks * lda, BKC ? ks : ks * ldb, e.ldd * n * 4};
+  if (at == E5MA_E5M2) return bt == E5MA_E5M2 ? run_d<E5MA_E5M2, E5MA_E5M2, AKC, BKC>(t, e, s) : run_d<E5MA_E5M2, E5MA_E4M3, AKC, BKC>(t, e, s);
   return bt == E5MA_E5M2 ? run_d<E5MA_E4M3, E5MA_E5M2, AKC, BKC>(t, e, s) : run_d<E5MA_E4M3, E5MA_E4M3, AKC, BKC>(t, e, s);
 }
 

@@ -188,8 +188,9 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_h_kernel(TileArgs t, Epilogu
   __shared__ float red[kThreads / 64];
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
-  int tm, tn;
-  tile_of(blockIdx.x, t.tiles_m, t.tiles_n, tm, tn);
+  int tm, tn, sp;
+  tile_of(blockIdx.x, t, tm, tn, sp);
+  apply_split(t, e, sp);
   const int i0 = tm * kBM, j0 = tn * kBN;
   const int nk = t.k / C::KS;
 
@@ -237,7 +238,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_h_kernel(TileArgs t, Epilogu
 
 template <int AT, int BT, bool AKC, bool BKC>
 hipError_t run_d(const TileArgs &t, const Epilogue &e, hipStream_t s) {
-  const int grid = t.tiles_m * t.tiles_n;
+  const int grid = t.tiles_m * t.tiles_n * t.splits;
   const int vec = ((uintptr_t)e.d % (4 * elem_bytes(e.d_dtype))) == 0 && e.ldd % 4 == 0 &&
                   (!e.sa_vec || (uintptr_t)e.sa % 16 == 0);
   const int simple = e.bias == nullptr && e.beta == 0.f && vec;
@@ -253,11 +254,13 @@ hipError_t run_d(const TileArgs &t, const Epilogue &e, hipStream_t s) {
   return hipGetLastError();
 }
 
-// the FP8 A x FP8 B pairings for one layout pair (lda / ldb in elements)
+// the FP8 A x FP8 B pairings for one layout pair (lda / ldb in elements; splits as in the FP8 kernel)
 template <bool AKC, bool BKC>
 hipError_t launch_layout(int at, int bt, const uint8_t *A, long long lda, const uint8_t *B, long long ldb, int m, int n,
-                         int k, const Epilogue &e, hipStream_t s) {
-  TileArgs t{A, B, lda, ldb, m, n, k, (m + kBM - 1) / kBM, (n + kBN - 1) / kBN};
+                         int k, int splits, const Epilogue &e, hipStream_t s) {
+  const int ks = k / splits;
+  TileArgs t{A, B, lda, ldb, m, n, ks, (m + kBM - 1) / kBM, (n + kBN - 1) / kBN, splits,
+             AKC ? ks : ks * lda, BKC ? ks : ks * ldb, e.ldd * n * 4};
   if (at == E5MA_E5M2)
     return bt == E5MA_E5M2 ? run_d<E5MA_E5M2, E5MA_E5M2, AKC, BKC>(t, e, s) : run_d<E5MA_E5M2, E5MA_E4M3, AKC, BKC>(t, e, s);
   return bt == E5MA_E5M2 ? run_d<E5MA_E4M3, E5MA_E5M2, AKC, BKC>(t, e, s) : run_d<E5MA_E4M3, E5MA_E4M3, AKC, BKC>(t, e, s);
@@ -266,8 +269,10 @@ hipError_t launch_layout(int at, int bt, const uint8_t *A, long long lda, const 
 // FP8 A x K-contiguous BF16 B (ldb in elements)
 template <bool AKC>
 hipError_t launch_layout_bf16(int at, int, const uint8_t *A, long long lda, const uint8_t *B, long long ldb, int m, int n,
-                              int k, const Epilogue &e, hipStream_t s) {
-  TileArgs t{A, B, lda, 2 * ldb, m, n, k, (m + kBM - 1) / kBM, (n + kBN - 1) / kBN};
+                              int k, int splits, const Epilogue &e, hipStream_t s) {
+  const int ks = k / splits;
+  TileArgs t{A, B, lda, 2 * ldb, m, n, ks, (m + kBM - 1) / kBM, (n + kBN - 1) / kBN, splits,
+             AKC ? ks : ks * lda, 2LL * ks, e.ldd * n * 4};
   return at == E5MA_E5M2 ? run_d<E5MA_E5M2, E5MA_BF16, AKC, true>(t, e, s) : run_d<E5MA_E4M3, E5MA_BF16, AKC, true>(t, e, s);
 }
 

@@ -59,21 +59,36 @@ template <int N> __device__ __forceinline__ void wait_barrier() {
 struct TileArgs {
   const uint8_t *A, *B;
   long long lda, ldb;  // in bytes
-  int m, n, k;
+  int m, n, k;         // k: the K range of one block (of one split)
   int tiles_m, tiles_n;
+  int splits;                 // K splits (1: none); split s writes FP32 partials at D + s * d_split
+  long long a_split, b_split;  // bytes from one split's first A / B element to the next split's
+  long long d_split;          // bytes between the splits' partial outputs
 };
 
-// output tile of block b: XCD-aware when the tile count is a multiple of 8 (blocks are dispatched to
-// the 8 XCDs round-robin), then grouped kGroupM m-tiles at a time
-__device__ __forceinline__ void tile_of(int b, int tiles_m, int tiles_n, int &tm, int &tn) {
-  const int total = tiles_m * tiles_n;
-  int t = b;
-  if ((total & 7) == 0) t = (b & 7) * (total >> 3) + (b >> 3);
-  const int per_group = kGroupM * tiles_n;
-  const int g = t / per_group, r = t - g * per_group;
-  const int gm = min(kGroupM, tiles_m - g * kGroupM);
+// Output tile and K split of block b.  XCD-aware when the block count is a multiple of 8 (blocks are
+// dispatched to the 8 XCDs round-robin): an XCD runs consecutive indices x, so with K splits each XCD
+// works on one split (one K slice of the operands in its L2); then tiles are grouped kGroupM m-tiles
+// at a time.
+__device__ __forceinline__ void tile_of(int b, const TileArgs &t, int &tm, int &tn, int &split) {
+  const int tiles = t.tiles_m * t.tiles_n, total = tiles * t.splits;
+  int x = b;
+  if ((total & 7) == 0) x = (b & 7) * (total >> 3) + (b >> 3);
+  split = x / tiles;
+  x -= split * tiles;
+  const int per_group = kGroupM * t.tiles_n;
+  const int g = x / per_group, r = x - g * per_group;
+  const int gm = min(kGroupM, t.tiles_m - g * kGroupM);
   tm = g * kGroupM + r % gm;
   tn = r / gm;
+}
+
+// the operands and output of K split s
+__device__ __forceinline__ void apply_split(TileArgs &t, Epilogue &e, int s) {
+  if (s == 0) return;
+  t.A += s * t.a_split;
+  t.B += s * t.b_split;
+  e.d = (uint8_t *)e.d + s * t.d_split;
 }
 
 // One direct-to-LDS load: 16 bytes per lane from src land at lds + 16 * lane (lds wave-uniform).

@@ -351,3 +351,41 @@ def test_h_config3_fp8_x_bf16_sampled(dev):
     assert s == 0
     bad, first = case.check(D, samples=4096, rng=rng)
     assert bad == 0, first
+
+
+# ---- split-K: outputs with at most half as many 256 x 256 tiles as CUs split K into FP32 partials that
+# a reduce kernel sums in order and runs through the epilogue (most fast-kernel tests above are such
+# shapes); these check the unsplit kernels (more than 128 tiles) and split counts at the edges ---------
+@pytest.mark.parametrize("ta,tb", [(1, 0), (0, 0)])
+def test_fast_unsplit_f8_sampled(dev, ta, tb):
+    rng = np.random.default_rng(9700 + ta * 2 + tb)
+    case = gu.GemmCase(rng, ta, tb, 4096, 4096, 8192, E5, E4, ddt=B16, dist="normal", sigma=8.0, sa=1 / 64,
+                       sb=1 / 64, pad=0)
+    s, D, _ = case.run(dev)
+    assert s == 0
+    bad, first = case.check(D, samples=4096, rng=rng)
+    assert bad == 0, first
+
+
+def test_fast_unsplit_h_sampled(dev):
+    rng = np.random.default_rng(9800)
+    case = gu.GemmCase(rng, 1, 0, 4096, 3072, 1024, E4, B16, ddt=F32, dist="normal", sigma=2.0, sa=0.5, pad=0,
+                       biasdt=F32, beta=0.5, cdt=B16)
+    s, D, _ = case.run(dev)
+    assert s == 0
+    bad, first = case.check(D, samples=4096, rng=rng)
+    assert bad == 0, first
+
+
+@pytest.mark.parametrize("m,n,k,adt,bdt", [(8192, 32, 8192, E5, E4), (256, 256, 16384, E4, E5),
+                                            (1024, 8192, 8192, E5, E5), (64, 48, 512, E5, E4),
+                                            (130, 20, 768, E4, B16)])
+def test_splitk_shapes(dev, m, n, k, adt, bdt):
+    """Skinny, tiny and half-filled grids (split counts 8, 32, 2, 1 and 3), FP8 output with amax."""
+    rng = np.random.default_rng(m + n + k)
+    case = gu.GemmCase(rng, 1, 0, m, n, k, adt, bdt, ddt=E5, qscale=0.5, amax=True, dist="normal", sigma=2.0,
+                       sa=0.25, pad=0 if m * n > 10**6 else 16)
+    s, D, amax = case.run(dev)
+    assert s == 0
+    bad, first = case.check(D, amax, samples=4096 if m * n > 10**6 else None, rng=rng)
+    assert bad == 0, first
