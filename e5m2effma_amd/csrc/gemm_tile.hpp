@@ -170,6 +170,79 @@ __device__ __forceinline__ float general_half(const Epilogue &e, const EpiState 
   return mx;
 }
 
+// Four BF16 codes (v[0] in the lowest half) by the hardware's pair conversion v_cvt_pk_bf16_f32: checked
+// here against the integer round-to-nearest-even encoder over all 2^32 FP32 inputs, identical except for
+// NaNs, which it keeps NaN but with their sign and payload.  Every NaN must become 0x7FC0
+// (include/e5m2effma.h, reference rne_hi), so lanes holding one take a rarely executed fix-up: the
+// common path is 4 compares and 2 conversions per 4 values (the integer encoder costs about 6 per value).
+__device__ __forceinline__ uint2 bf16_quad(const float (&v)[4]) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  uint32_t lo = __builtin_bit_cast(uint32_t, bf16x2_t{(__bf16)v[0], (__bf16)v[1]});
+  uint32_t hi = __builtin_bit_cast(uint32_t, bf16x2_t{(__bf16)v[2], (__bf16)v[3]});
+  // the flags are taken before the branch, so the values are dead across it (else they are spilled)
+  const bool n0 = v[0] != v[0], n1 = v[1] != v[1], n2 = v[2] != v[2], n3 = v[3] != v[3];
+  if (n0 || n1 || n2 || n3) {
+    if (n0) lo = (lo & 0xFFFF0000u) | 0x7FC0u;
+    if (n1) lo = (lo & 0x0000FFFFu) | 0x7FC00000u;
+    if (n2) hi = (hi & 0xFFFF0000u) | 0x7FC0u;
+    if (n3) hi = (hi & 0x0000FFFFu) | 0x7FC00000u;
+  }
+  return make_uint2(lo, hi);
+}
+
+// The direct epilogue of a full tile with no bias and beta = 0: scale, convert and store straight from
+// the accumulators, column by column (y outer): the 16 stores into one column's cache lines follow each
+// other, so the L2 writes the lines back whole (x / g outer measured 3x the write traffic).  AMAX: fold
+// |value| for amax (compiled out otherwise: the epilogue is VALU-bound with one wave per SIMD).
+template <int DT, bool AMAX>
+__device__ __forceinline__ float direct_epilogue(const Epilogue &e, v16f (&acc)[4][4], int i0, int j0, int wm, int wn,
+                                                 int lane) {
+  float mx = 0.f;
+  const EpiState st = epi_begin(e);
+  const int ib0 = i0 + 128 * wm + 4 * (lane >> 5);
+  const float sa1 = e.alpha * scale_or_one(e.sa), sb1 = scale_or_one(e.sb);
+#pragma unroll
+  for (int y = 0; y < 4; ++y) {
+    const int j = j0 + 128 * wn + 32 * y + (lane & 31);
+    const float sbj = e.sb_vec ? e.sb[j] : sb1;
+    uint8_t *colp = (uint8_t *)e.d + ((size_t)j * e.ldd + ib0) * elem_bytes(DT);
+#pragma unroll
+    for (int x = 0; x < 4; ++x)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        __builtin_amdgcn_sched_barrier(0);
+        const int ib = ib0 + 32 * x + 8 * g;
+        float as[4];  // alpha * sa[i] of these 4 rows (OUTER scaling of A)
+        if (e.sa_vec) {
+          const float4 v = *(const float4 *)(e.sa + ib);
+          as[0] = e.alpha * v.x; as[1] = e.alpha * v.y; as[2] = e.alpha * v.z; as[3] = e.alpha * v.w;
+        } else {
+          as[0] = as[1] = as[2] = as[3] = sa1;
+        }
+        float v[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const float sc = (e.sa_vec || e.sb_vec) ? as[q] * sbj : st.s;
+          v[q] = acc_read(acc[x][y][4 * g + q]) * sc;
+          if constexpr (AMAX) mx = amax_fold(mx, v[q]);
+        }
+        uint8_t *dp = colp + (32 * x + 8 * g) * elem_bytes(DT);
+        if constexpr (DT == E5MA_FP32) {
+          *(float4 *)dp = make_float4(v[0], v[1], v[2], v[3]);
+        } else if constexpr (is_fp8(DT)) {
+          *(uint32_t *)dp = encode_t<DT>(v[0], st.qscale) | encode_t<DT>(v[1], st.qscale) << 8 |
+                            encode_t<DT>(v[2], st.qscale) << 16 | encode_t<DT>(v[3], st.qscale) << 24;
+        } else if constexpr (DT == E5MA_BF16) {
+          *(uint2 *)dp = bf16_quad(v);
+        } else {
+          *(uint2 *)dp = make_uint2(encode_t<DT>(v[0], 1.f) | encode_t<DT>(v[1], 1.f) << 16,
+                                    encode_t<DT>(v[2], 1.f) | encode_t<DT>(v[3], 1.f) << 16);
+        }
+      }
+  }
+  return mx;
+}
+
 // The epilogue of a block tile (acc: this wave's accumulators; i0, j0: the tile's origin).  Returns the
 // thread's max |value| for amax.
 template <int DT>
@@ -182,51 +255,9 @@ __device__ __forceinline__ float tile_epilogue(const TileArgs &t, const Epilogue
   __builtin_amdgcn_sched_barrier(0);
   float mx = 0.f;
   if (simple && i0 + kBM <= t.m && j0 + kBN <= t.n) {
-    // no bias, beta = 0, a full tile, D aligned for 4-element stores: scale, convert and store straight
-    // from the accumulators (no tail branches, so every loop unrolls and the accumulators stay in
-    // registers)
-    const EpiState st = epi_begin(e);
-    const int ib0 = i0 + 128 * wm + 4 * (lane >> 5);
-    const float sa1 = e.alpha * scale_or_one(e.sa), sb1 = scale_or_one(e.sb);
-    // column by column (y outer): the 16 stores into one column's cache lines follow each other, so
-    // the L2 writes the lines back whole (x / g outer measured 3x the write traffic)
-#pragma unroll
-    for (int y = 0; y < 4; ++y) {
-      const int j = j0 + 128 * wn + 32 * y + (lane & 31);
-      const float sbj = e.sb_vec ? e.sb[j] : sb1;
-      uint8_t *colp = (uint8_t *)e.d + ((size_t)j * e.ldd + ib0) * elem_bytes(DT);
-#pragma unroll
-      for (int x = 0; x < 4; ++x)
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          __builtin_amdgcn_sched_barrier(0);
-          const int ib = ib0 + 32 * x + 8 * g;
-          float as[4];  // alpha * sa[i] of these 4 rows (OUTER scaling of A)
-          if (e.sa_vec) {
-            const float4 v = *(const float4 *)(e.sa + ib);
-            as[0] = e.alpha * v.x; as[1] = e.alpha * v.y; as[2] = e.alpha * v.z; as[3] = e.alpha * v.w;
-          } else {
-            as[0] = as[1] = as[2] = as[3] = sa1;
-          }
-          float v[4];
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const float sc = (e.sa_vec || e.sb_vec) ? as[q] * sbj : st.s;
-            v[q] = acc_read(acc[x][y][4 * g + q]) * sc;
-            mx = amax_fold(mx, v[q]);
-          }
-          uint8_t *dp = colp + (32 * x + 8 * g) * elem_bytes(DT);
-          if constexpr (DT == E5MA_FP32) {
-            *(float4 *)dp = make_float4(v[0], v[1], v[2], v[3]);
-          } else if constexpr (is_fp8(DT)) {
-            *(uint32_t *)dp = encode_t<DT>(v[0], st.qscale) | encode_t<DT>(v[1], st.qscale) << 8 |
-                              encode_t<DT>(v[2], st.qscale) << 16 | encode_t<DT>(v[3], st.qscale) << 24;
-          } else {
-            *(uint2 *)dp = make_uint2(encode_t<DT>(v[0], 1.f) | encode_t<DT>(v[1], 1.f) << 16,
-                                      encode_t<DT>(v[2], 1.f) | encode_t<DT>(v[3], 1.f) << 16);
-          }
-        }
-    }
+    // no bias, beta = 0, a full tile, D aligned for 4-element stores
+    mx = e.amax ? direct_epilogue<DT, true>(e, acc, i0, j0, wm, wn, lane)
+                : direct_epilogue<DT, false>(e, acc, i0, j0, wm, wn, lane);
   } else {
     // general epilogue (bias, beta * C, tails): half a tile at a time -- the 128 columns of the waves
     // with wn == h, 256 x 128 FP32 = the whole ring, column group c (16 columns) in ring buffer c --

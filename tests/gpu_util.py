@@ -57,19 +57,22 @@ def operand(rng, dt, size, dist="codes", sigma=1.0):
 class GemmCase:
     """One e5ma_gemm call: seeded operands, the GPU run through the C ABI, the oracle check.
 
-    transa / transb: 1 = T.  sa / sb: None, a float (per tensor) or an array (OUTER scaling).
+    transa / transb: 1 = T.  sa / sb: None, a float (per tensor) or an array (OUTER scaling).  ldd: leading
+    dimension of D (default m + 3).
     beta != 0 with cdt None accumulates into D (C = NULL); otherwise C of dtype cdt is read."""
 
     def __init__(self, rng, transa, transb, m, n, k, adt, bdt, *, ddt=oracle.FP32, alpha=1.0, sa=None, sb=None,
                  beta=0.0, cdt=None, csinv=1.0, biasdt=None, qscale=None, amax=False, pad=16, dist="codes",
-                 sigma=1.0, A=None, B=None, D0=None):
+                 sigma=1.0, A=None, B=None, D0=None, ldd=None):
         self.transa, self.transb, self.m, self.n, self.k = transa, transb, m, n, k
         self.adt, self.bdt, self.ddt, self.alpha, self.beta = adt, bdt, ddt, alpha, beta
         self.lda = (k if transa else m) + pad
         self.ldb = (n if transb else k) + pad
         self.lda = (self.lda + 15) // 16 * 16
         self.ldb = (self.ldb + 15) // 16 * 16
-        self.ldd = m + (3 if m > 1 else 0)
+        # default ldd = m + 3 (padding rows catch stray writes; not a multiple of 4, so the kernels take their
+        # general epilogue); ldd = m + 4 with m % 4 == 0 keeps the padding and allows the direct epilogue
+        self.ldd = ldd if ldd is not None else m + (3 if m > 1 else 0)
         self.A = A if A is not None else operand(rng, adt, self.lda * (m if transa else k), dist, sigma)
         self.B = B if B is not None else operand(rng, bdt, self.ldb * (k if transb else n), dist, sigma)
         self.sa, self.sb = sa, sb

@@ -389,3 +389,55 @@ def test_splitk_shapes(dev, m, n, k, adt, bdt):
     assert s == 0
     bad, first = case.check(D, amax, samples=4096 if m * n > 10**6 else None, rng=rng)
     assert bad == 0, first
+
+
+def test_direct_epilogue_bf16_nan_codes(dev):
+    """The direct epilogue's hardware BF16 conversion keeps a NaN's sign and payload; every NaN output
+    must still be 0x7FC0.  Unsplit grid (81 tiles), BF16 output, no bias, beta = 0: NaN (0x7F, 0xFE) and
+    Inf (0x7C) codes of A make rows 5, 6 NaN and row 9 Inf or NaN; sampled oracle check elsewhere."""
+    rng = np.random.default_rng(9900)
+    m = n = 2304
+    k = 1024
+    case = gu.GemmCase(rng, 1, 0, m, n, k, E5, B16, ddt=B16, dist="normal", sigma=1.0, pad=0, ldd=m + 4)
+    A = case.A.copy()
+    A[5 * k + 7] = 0x7F   # NaN
+    A[6 * k + 3] = 0xFE   # negative NaN
+    A[9 * k + 1] = 0x7C   # +Inf
+    case.A = A
+    s, D, _ = case.run(dev)
+    assert s == 0
+    Dm = D.view(np.uint16).reshape(n, case.ldd)[:, :m]
+    assert (Dm[:, 5] == 0x7FC0).all() and (Dm[:, 6] == 0x7FC0).all()
+    r9 = Dm[:, 9]
+    assert (((r9 & 0x7FFF) == 0x7F80) | (r9 == 0x7FC0)).all()
+    bad, first = case.check(D, samples=4096, rng=rng)
+    assert bad == 0, first
+
+
+# ---- the direct epilogue (full tiles, no bias, beta = 0, D columns 16-byte aligned: ldd % 4 == 0) on
+# unsplit grids (more than 64 tiles), every output dtype, outer scales, amax ---------------------------
+@pytest.mark.parametrize("ddt", [B16, F16, F32, E5, E4])
+@pytest.mark.parametrize("ta,tb", LAYOUTS)
+def test_direct_epilogue_f8(dev, ta, tb, ddt):
+    rng = np.random.default_rng(10000 + ta * 2 + tb + 10 * ddt)
+    m, n, k = 2304, 2048, 8192
+    sa = rng.uniform(0.5, 2.0, m).astype(np.float32) * (1 / 64)
+    sb = rng.uniform(0.5, 2.0, n).astype(np.float32) * (1 / 64)
+    case = gu.GemmCase(rng, ta, tb, m, n, k, E5, E4, ddt=ddt, alpha=0.5, sa=sa, sb=sb, dist="normal", sigma=8.0,
+                       pad=0, ldd=m + 4, amax=True, qscale=0.25 if ddt in (E5, E4) else None)
+    s, D, amax = case.run(dev)
+    assert s == 0
+    bad, first = case.check(D, amax, samples=4096, rng=rng)
+    assert bad == 0, first
+
+
+@pytest.mark.parametrize("bdt", [B16, E5])
+def test_direct_epilogue_h(dev, bdt):
+    rng = np.random.default_rng(10100 + bdt)
+    m, n, k = 2304, 2304, 1024
+    case = gu.GemmCase(rng, 1, 0, m, n, k, E4, bdt, ddt=B16, sa=0.5, sb=0.25 if bdt == E5 else None,
+                       dist="normal", sigma=2.0, pad=0, ldd=m + 4)
+    s, D, _ = case.run(dev)
+    assert s == 0
+    bad, first = case.check(D, samples=4096, rng=rng)
+    assert bad == 0, first
