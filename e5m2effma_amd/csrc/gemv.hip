@@ -303,14 +303,18 @@ __global__ __launch_bounds__(kThreads) void gemv_dot_kernel(const uint8_t *A, lo
   if (e.amax) amax_commit_block(e.amax, mx, red);
 }
 
-// ---- x staged in LDS by direct-to-LDS loads (n <= 2, k * n * bytes(x) <= kXLds) ----------------
-constexpr int kXLds = 32768;
+// ---- x staged in LDS by direct-to-LDS loads (BF16 / FP16 / FP8 x of at most kXLds bytes) ----------
+constexpr int kXLds = 131072;
 #ifndef E5MA_GEMV_RX
 #define E5MA_GEMV_RX 2  // rows per wave
 #endif
 #ifndef E5MA_GEMV_UX
 #define E5MA_GEMV_UX 4  // 16-byte chunks per lane and row in flight
 #endif
+// n > 2 (measured on 8192^2: n = 4 best with 2 rows x 2 chunks, 16.5 us; n = 8 with 4 rows x 2 chunks,
+// 24.6 us, where the FP32 FMA kernel took 24.1 / 34.1 us; 2 rows x 4 chunks spill at n = 8)
+template <int NB> constexpr int kGemvRxWide = NB <= 4 ? 2 : 4;
+constexpr int kGemvUxWide = 2;
 typedef __attribute__((address_space(3))) void lds_void_t;
 
 // one direct-to-LDS load: 16 bytes per lane from src to lds + 16 * lane (lds wave-uniform); inline asm,
@@ -437,24 +441,28 @@ __global__ __launch_bounds__(kXThreads) void gemv_xlds_kernel(const uint8_t *A, 
 template <int AT, int BT, int NB>
 hipError_t gemv_n(const uint8_t *A, long long lda, const uint8_t *B, long long ldb, int m, int k, const Epilogue &e,
                   hipStream_t s) {
-  if constexpr (BT != E5MA_FP32 && NB <= 2) {
-    constexpr int R = E5MA_GEMV_R_NARROW, U = E5MA_GEMV_U_NARROW;
-    const int grid = (m + kWaves * R - 1) / (kWaves * R);
+  if constexpr (BT != E5MA_FP32) {
     const long long xbytes = (long long)k * NB * elem_bytes(BT);
     if (xbytes <= kXLds) {
-      constexpr int RX = E5MA_GEMV_RX, UX = E5MA_GEMV_UX;
+      constexpr int RX = NB <= 2 ? E5MA_GEMV_RX : kGemvRxWide<NB>, UX = NB <= 2 ? E5MA_GEMV_UX : kGemvUxWide;
       const int gx = (m + kXWaves * RX - 1) / (kXWaves * RX);
       const size_t lds = (size_t)((xbytes + 1023) / 1024 * 1024);
       gemv_xlds_kernel<AT, BT, NB, RX, UX><<<gx, kXThreads, lds, s>>>(A, lda, B, ldb, m, k, e);
-    } else
+      return hipGetLastError();
+    }
+    if constexpr (NB <= 2) {
+      constexpr int R = E5MA_GEMV_R_NARROW, U = E5MA_GEMV_U_NARROW;
+      const int grid = (m + kWaves * R - 1) / (kWaves * R);
       gemv_dot_kernel<AT, BT, NB, R, U><<<grid, kThreads, 0, s>>>(A, lda, B, ldb, m, k, e);
-  } else {  // FP32 x is not a BF16 value, and for wider x the FP32 FMA kernel measured faster
-    constexpr int R = NB <= 2 ? 4 : 2;
-    constexpr int U = NB <= 2 ? 4 : 2;
-    const int rows_per_block = kWaves * R;
-    const int grid = (m + rows_per_block - 1) / rows_per_block;
-    gemv_kernel<AT, BT, NB, R, U><<<grid, kThreads, 0, s>>>(A, lda, B, ldb, m, k, e);
+      return hipGetLastError();
+    }
   }
+  // FP32 x is not a BF16 value; a wide x that does not fit LDS: the FP32 FMA kernel
+  constexpr int R = NB <= 2 ? 4 : 2;
+  constexpr int U = NB <= 2 ? 4 : 2;
+  const int rows_per_block = kWaves * R;
+  const int grid = (m + rows_per_block - 1) / rows_per_block;
+  gemv_kernel<AT, BT, NB, R, U><<<grid, kThreads, 0, s>>>(A, lda, B, ldb, m, k, e);
   return hipGetLastError();
 }
 
