@@ -102,37 +102,70 @@ __device__ __forceinline__ void load_lds16(const uint8_t *src, const uint8_t *ld
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(l) : "memory", "m0");
 }
 
+// Four consecutive elements of dtype T at element idx (4-element aligned) as FP32 (FP8 times sinv; the
+// others exact): one vector load
+template <int T> __device__ __forceinline__ void load4_t(const void *p, size_t idx, float sinv, float (&o)[4]) {
+  const uint8_t *b = (const uint8_t *)p + idx * elem_bytes(T);
+  if constexpr (T == E5MA_FP32) {
+    const float4 v = *(const float4 *)b;
+    o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
+  } else if constexpr (elem_bytes(T) == 2) {
+    const uint2 v = *(const uint2 *)b;
+    const uint32_t h[4] = {v.x & 0xFFFFu, v.x >> 16, v.y & 0xFFFFu, v.y >> 16};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) o[q] = T == E5MA_BF16 ? bf16_value(h[q]) : f16_value(h[q]);
+  } else {
+    const uint32_t v = *(const uint32_t *)b;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t c = (v >> (8 * q)) & 0xFFu;
+      o[q] = (T == E5MA_E5M2 ? e5m2_value(c) : e4m3_value(c)) * sinv;
+    }
+  }
+}
+
 // Writes out one staged half tile (256 rows x 128 columns starting at column jh) in the reference's
 // epilogue order (include/e5m2effma.h: v = acc * (alpha * sa[i]) * sb[j]; v += bias[i];
 // v = fma(beta, C * csinv, v); amax; convert).  Wave w takes columns w, w + 4, ..., thread t rows
-// i .. i + 3 (i = i0 + 4 (t % 64)); four columns per step, with their C values loaded before any is
-// computed or stored, so 16 loads per thread are in flight (C may alias D: each element is read before
-// it is written, by the same thread).  CT: the dtype of C, or -1 when beta = 0.
+// i .. i + 3 (i = i0 + 4 (t % 64)); eight columns per step, with their C values loaded (one vector load
+// per column when C is aligned) before any is computed or stored, so 32 values per thread are in
+// flight (C may alias D: each element is read before it is written, by the same thread).  CT: the
+// dtype of C, or -1 when beta = 0.
 template <int DT, int CT>
 __device__ __forceinline__ float general_half(const Epilogue &e, const EpiState &st, const TileArgs &t, int i, int jh,
                                               const float (&rs)[4], const float (&rb)[4], int vec, int tid,
                                               float mx) {
+  constexpr int kCols = 8;  // columns per step
   const int w = tid >> 6, il = 4 * (tid & 63);
   const bool rows4 = i + 3 < t.m;
+  bool cvec = false;
+  if constexpr (CT >= 0)
+    cvec = rows4 && (uintptr_t)e.c % (4 * elem_bytes(CT)) == 0 && e.ldc % 4 == 0;
   const float sb1 = scale_or_one(e.sb);
 #pragma unroll 1
-  for (int c0 = 0; c0 < 32; c0 += 4) {
-    float a[4][4], cv[4][4];
+  for (int c0 = 0; c0 < 32; c0 += kCols) {
+    float a[kCols][4], cv[kCols][4];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < kCols; ++u) {
       const int jl = w + 4 * (c0 + u), j = jh + jl;
       const float4 v4 = *(const float4 *)(stage_at(jl >> 4) + (jl & 15) * kBM + il);
       a[u][0] = v4.x; a[u][1] = v4.y; a[u][2] = v4.z; a[u][3] = v4.w;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        cv[u][q] = 0.f;
-        if constexpr (CT >= 0) {
-          if (j < t.n && i + q < t.m) cv[u][q] = load_t<CT>(e.c, (size_t)j * e.ldc + i + q, st.csinv);
+      for (int q = 0; q < 4; ++q) cv[u][q] = 0.f;
+      if constexpr (CT >= 0) {
+        if (j < t.n) {
+          if (cvec) {
+            load4_t<CT>(e.c, (size_t)j * e.ldc + i, st.csinv, cv[u]);
+          } else {
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+              if (i + q < t.m) cv[u][q] = load_t<CT>(e.c, (size_t)j * e.ldc + i + q, st.csinv);
+          }
         }
       }
     }
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < kCols; ++u) {
       const int j = jh + w + 4 * (c0 + u);
       if (j >= t.n) continue;
       const float sbj = e.sb_vec ? e.sb[j] : sb1;
