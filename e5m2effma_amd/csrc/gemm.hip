@@ -99,7 +99,7 @@ hipError_t launch_fast(FastLaunch launch, int round, int at, int bt, bool akc, b
 hipError_t launch_gemm(int at, int bt, bool akc, bool bkc, const uint8_t *A, long long lda, const uint8_t *B,
                        long long ldb, int m, int n, int k, const dev::Epilogue &e, const DeviceInfo &di,
                        hipStream_t s) {
-  if (gemm_f8_applies(at, bt, akc, bkc, m, n, k))
+  if (gemm_f8_applies(at, bt, akc, bkc, m, n, k, lda, ldb))
     return launch_fast(launch_gemm_f8, gemm_f8_round(), at, bt, akc, bkc, A, lda, B, ldb, m, n, k, e, di, s);
   if (gemm_h_applies(at, bt, akc, bkc, m, n, k))
     return launch_fast(launch_gemm_h, gemm_h_round(bt), at, bt, akc, bkc, A, lda, B, ldb, m, n, k, e, di, s);

@@ -112,8 +112,12 @@ __device__ __attribute__((noinline)) float epilogue_block(const dev::Epilogue &e
 
 }  // namespace gemm
 
+// largest leading dimension (bytes) of an operand of the fast kernels: their direct-to-LDS loads
+// address a stage as a wave-uniform base plus 32-bit per-lane offsets of up to 255 rows
+constexpr long long kMaxLd = 1LL << 24;
+
 // fast FP8 x FP8 path (gemm_f8.hip), any operand layout; akc / bkc: A / B K-contiguous
-bool gemm_f8_applies(int at, int bt, bool akc, bool bkc, int m, int n, int k);
+bool gemm_f8_applies(int at, int bt, bool akc, bool bkc, int m, int n, int k, long long lda, long long ldb);
 hipError_t launch_gemm_f8(int at, int bt, bool akc, bool bkc, const uint8_t *A, long long lda, const uint8_t *B,
                           long long ldb, int m, int n, int k, int splits, const dev::Epilogue &e, hipStream_t s);
 // its instances, one translation unit per layout pair, named for (transa, transb):

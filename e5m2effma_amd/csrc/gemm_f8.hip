@@ -9,11 +9,11 @@ namespace {
 constexpr int kRound = 256;  // the K loop runs whole rounds of the 4-slot ring of 64-byte stages
 }
 
-bool gemm_f8_applies(int at, int bt, bool akc, bool bkc, int m, int n, int k) {
+bool gemm_f8_applies(int at, int bt, bool akc, bool bkc, int m, int n, int k, long long lda, long long ldb) {
   // at least 2 rounds; an M / N-contiguous operand is loaded in whole 16-byte chunks of its rows, so its
-  // m (n) is a multiple of 16
+  // m (n) is a multiple of 16; the loads' 32-bit per-lane offsets need lda, ldb <= kMaxLd bytes
   return is_fp8(at) && is_fp8(bt) && k % kRound == 0 && k >= 2 * kRound && gemm::mode_of(at, bt, k) == gemm::kModeF8 &&
-         m > 0 && n > 0 && (akc || m % 16 == 0) && (bkc || n % 16 == 0);
+         m > 0 && n > 0 && (akc || m % 16 == 0) && (bkc || n % 16 == 0) && lda <= kMaxLd && ldb <= kMaxLd;
 }
 
 hipError_t launch_gemm_f8(int at, int bt, bool akc, bool bkc, const uint8_t *A, long long lda, const uint8_t *B,

@@ -6,10 +6,12 @@
 // translation unit per layout pair (gemm_f8_tn/nn/nt/tt.hip), which build in parallel.
 //
 // Block tile 256 x 256, 4 waves (one per SIMD), each owning a 128 x 128 sub-tile held as 4 x 4
-// accumulator blocks of v_mfma_scale_f32_32x32x64_f8f6f4 (256 accumulator registers per lane).
+// accumulator blocks of v_mfma_f32_32x32x64_f8f6f4 (256 accumulator registers per lane).
 // K advances in stages of 64 bytes.  A 4-slot LDS ring (4 x 32 KiB, one object per slot and operand)
 // is filled by direct-to-LDS loads (global_load_lds_dwordx4: 64 lanes x 16 bytes land contiguously,
-// no VGPR staging) issued three stages ahead; each stage costs one barrier.  The fragments are
+// no VGPR staging) issued three stages ahead; each stage costs one barrier.  The loads address a stage
+// as a scalar base (advanced per stage) plus per-lane offsets fixed for the whole K loop, so the loop
+// issues no vector ALU instructions besides the MFMAs.  The fragments are
 // single-buffered (64 VGPRs beside the 256 accumulator registers) and the stage loop is unrolled by 4
 // so that ring slots are compile-time indices.  Within a stage the MFMAs, the fragment reads of the
 // next stage and the loads of stage s + 4 are interleaved.
@@ -44,36 +46,63 @@ constexpr int kLoadsPerWave = kOpBytes / 1024 / 4; // dwordx4 LDS loads per wave
 
 __device__ __forceinline__ int swz(int r) { return (r >> 2) & 3; }
 
-// one 1 KiB direct-to-LDS load of an operand stage: block blk (of 16) of the slot.
-// K-contiguous source: rows r0 + 16 blk .. + 15, 64 K bytes each (rows past lim repeat row lim - 1).
-// M / N-contiguous source: k-rows 4 blk .. + 3 of the stage, 256 bytes of rows r0 .. r0 + 255 each
-// (chunks past lim, a multiple of 16, repeat the last chunk; never stored).
-template <bool KC>
-__device__ __forceinline__ void load_op(const uint8_t *P, long long ld, int lim, int kb, int r0, int blk, int lane,
-                                        uint8_t *lds) {
+// Per-lane byte offset, from the operand's stage base, of this lane's 16 bytes in the 1 KiB
+// direct-to-LDS load blk (of 16) of an operand stage.  Stage s's base is P + r0 * ld + s * kBK for a
+// K-contiguous operand and P + r0 + s * kBK * ld for an M / N-contiguous one, so the offsets are the
+// same for every stage.
+// K-contiguous: rows r0 + 16 blk .. + 15, 64 K bytes each (rows past lim repeat row lim - 1); 16-byte
+// chunk c of row r lands at chunk c ^ swz(r).
+// M / N-contiguous: k-rows 4 blk .. + 3 of the stage, 256 bytes of rows r0 .. r0 + 255 each (chunks
+// past lim, a multiple of 16, repeat the last chunk; never stored).
+// Offsets stay below 2^32 for ld <= kMaxLd (checked by the host).
+template <bool KC> __device__ __forceinline__ uint32_t op_offset(long long ld, int lim, int r0, int blk, int lane) {
   if constexpr (KC) {
     const int r = blk * 16 + (lane >> 2);
     const int c = (lane & 3) ^ swz(r);
-    load_lds16(P + (long long)min(r0 + r, lim - 1) * ld + kb + 16 * c, lds + blk * 1024);
+    return (uint32_t)(min(r0 + r, lim - 1) - r0) * (uint32_t)ld + 16 * c;
   } else {
     const int kk = blk * 4 + (lane >> 4);
     const int c = (lane & 15) ^ ((kk & 7) << 1);
-    load_lds16(P + (long long)(kb + kk) * ld + min(r0 + 16 * c, lim - 16), lds + blk * 1024);
+    return (uint32_t)kk * (uint32_t)ld + (uint32_t)(min(r0 + 16 * c, lim - 16) - r0);
   }
 }
 
-// load q (of kLoadsPerWave) of this wave's share of one stage: 1 KiB of A and 1 KiB of B into LDS
-// slot SLOT
-template <int SLOT, bool AKC, bool BKC>
-__device__ __forceinline__ void issue_load(const TileArgs &t, int kb, int i0, int j0, int wave, int lane, int q) {
-  const int blk = wave * kLoadsPerWave + q;
-  load_op<AKC>(t.A, t.lda, t.m, kb, i0, blk, lane, lds_a<SLOT>());
-  load_op<BKC>(t.B, t.ldb, t.n, kb, j0, blk, lane, lds_b<SLOT>());
-}
-template <int SLOT, bool AKC, bool BKC>
-__device__ __forceinline__ void issue_stage(const TileArgs &t, int kb, int i0, int j0, int wave, int lane) {
+// What the loads of one block need: the operands' stage-0 bases and per-stage strides (wave-uniform)
+// and this lane's offsets for its share (kLoadsPerWave loads per operand and stage)
+struct Loads {
+  const uint8_t *a, *b;
+  long long sa, sb;
+  uint32_t oa[kLoadsPerWave], ob[kLoadsPerWave];
+  uint32_t lds0;  // LDS offset of this wave's share within a buffer
+};
+
+template <bool AKC, bool BKC>
+__device__ __forceinline__ Loads make_loads(const TileArgs &t, int i0, int j0, int wave, int lane) {
+  Loads L;
+  L.a = uniform_ptr(t.A + (AKC ? (long long)i0 * t.lda : i0));
+  L.b = uniform_ptr(t.B + (BKC ? (long long)j0 * t.ldb : j0));
+  L.sa = AKC ? kBK : kBK * t.lda;
+  L.sb = BKC ? kBK : kBK * t.ldb;
 #pragma unroll
-  for (int q = 0; q < kLoadsPerWave; ++q) issue_load<SLOT, AKC, BKC>(t, kb, i0, j0, wave, lane, q);
+  for (int q = 0; q < kLoadsPerWave; ++q) {
+    L.oa[q] = op_offset<AKC>(t.lda, t.m, i0, wave * kLoadsPerWave + q, lane);
+    L.ob[q] = op_offset<BKC>(t.ldb, t.n, j0, wave * kLoadsPerWave + q, lane);
+  }
+  L.lds0 = wave * kLoadsPerWave * 1024;
+  return L;
+}
+
+// load q (of kLoadsPerWave) of this wave's share of stage s: 1 KiB of A and 1 KiB of B into LDS
+// slot SLOT
+template <int SLOT>
+__device__ __forceinline__ void issue_load(const Loads &L, int s, int q) {
+  load_lds16s(L.a + s * L.sa, L.oa[q], lds_addr(lds_a<SLOT>()) + L.lds0 + q * 1024);
+  load_lds16s(L.b + s * L.sb, L.ob[q], lds_addr(lds_b<SLOT>()) + L.lds0 + q * 1024);
+}
+template <int SLOT>
+__device__ __forceinline__ void issue_stage(const Loads &L, int s) {
+#pragma unroll
+  for (int q = 0; q < kLoadsPerWave; ++q) issue_load<SLOT>(L, s, q);
 }
 
 // fragments of one 32-row block of an operand stage: lane l holds the 32 K bytes
@@ -109,8 +138,8 @@ template <bool KC> __device__ __forceinline__ v8i read_frag(const uint8_t *s, in
 // exists.  The loads of stage s + 4 into stage s's slot (free: every wave read it before the barrier)
 // go out one pair after every fourth MFMA.  (Issuing the 8 loads as one burst stalled the MFMA stream.)
 template <int WAITN, bool NEXT, bool ISSUE, int SLOT, int AT, int BT, bool AKC, bool BKC>
-__device__ __forceinline__ void f8_stage(const TileArgs &t, int s, int i0, int j0, int wave, int lane, int wm, int wn,
-                                         v8i (&a)[2][4], v8i (&b)[2][4], v16f (&acc)[4][4]) {
+__device__ __forceinline__ void f8_stage(const Loads &L, int s, int lane, int wm, int wn, v8i (&a)[2][4],
+                                         v8i (&b)[2][4], v16f (&acc)[4][4]) {
   constexpr int P = SLOT & 1, Q = P ^ 1;
   if constexpr (NEXT) wait_barrier<WAITN>();
   const uint8_t *na = lds_a<(SLOT + 1) & 3>(), *nb = lds_b<(SLOT + 1) & 3>();
@@ -118,10 +147,12 @@ __device__ __forceinline__ void f8_stage(const TileArgs &t, int s, int i0, int j
   for (int x = 0; x < 4; ++x) {
 #pragma unroll
     for (int y = 0; y < 4; ++y) {
+      // scale operands 0 select the unscaled v_mfma_f32_32x32x64_f8f6f4 (same products as the scaled form
+      // with the neutral scale 127, one instruction dword pair shorter)
       acc[x][y] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a[P][x], b[P][y], acc[x][y], kMfmaFmt<AT>,
-                                                                  kMfmaFmt<BT>, 0, kNeutralScale, 0, kNeutralScale);
+                                                                  kMfmaFmt<BT>, 0, 0, 0, 0);
       if constexpr (ISSUE) {
-        if (y == 1) issue_load<SLOT, AKC, BKC>(t, (s + 4) * kBK, i0, j0, wave, lane, x);
+        if (y == 1) issue_load<SLOT>(L, s + 4, x);
       }
       if constexpr (NEXT) {
         const int i = 4 * x + y;  // fragment i / 2 of the next stage after MFMA i (i even)
@@ -163,11 +194,12 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_f8_kernel(TileArgs t, Epilog
       for (int r = 0; r < 16; ++r) acc[x][y][r] = 0.f;
 
   // prologue: stages 0..2 in flight; stage 3 is issued once every wave is past the first barrier
-  issue_stage<0, AKC, BKC>(t, 0 * kBK, i0, j0, wave, lane);
-  issue_stage<1, AKC, BKC>(t, 1 * kBK, i0, j0, wave, lane);
-  issue_stage<2, AKC, BKC>(t, 2 * kBK, i0, j0, wave, lane);
+  const Loads L = make_loads<AKC, BKC>(t, i0, j0, wave, lane);
+  issue_stage<0>(L, 0);
+  issue_stage<1>(L, 1);
+  issue_stage<2>(L, 2);
   wait_barrier<2 * 2 * kLoadsPerWave>();  // stage 0 landed; stages 1 and 2 may be in flight
-  issue_stage<3, AKC, BKC>(t, 3 * kBK, i0, j0, wave, lane);
+  issue_stage<3>(L, 3);
   v8i a[2][4], b[2][4];  // fragments, double-buffered by stage parity
 #pragma unroll
   for (int x = 0; x < 4; ++x) {
@@ -179,15 +211,15 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_f8_kernel(TileArgs t, Epilog
   constexpr int kW2 = 2 * 2 * kLoadsPerWave, kW1 = 2 * kLoadsPerWave;
   int s = 0;
   for (; s < nk - 4; s += 4) {
-    f8_stage<kW2, true, true, 0, AT, BT, AKC, BKC>(t, s, i0, j0, wave, lane, wm, wn, a, b, acc);
-    f8_stage<kW2, true, true, 1, AT, BT, AKC, BKC>(t, s + 1, i0, j0, wave, lane, wm, wn, a, b, acc);
-    f8_stage<kW2, true, true, 2, AT, BT, AKC, BKC>(t, s + 2, i0, j0, wave, lane, wm, wn, a, b, acc);
-    f8_stage<kW2, true, true, 3, AT, BT, AKC, BKC>(t, s + 3, i0, j0, wave, lane, wm, wn, a, b, acc);
+    f8_stage<kW2, true, true, 0, AT, BT, AKC, BKC>(L, s, lane, wm, wn, a, b, acc);
+    f8_stage<kW2, true, true, 1, AT, BT, AKC, BKC>(L, s + 1, lane, wm, wn, a, b, acc);
+    f8_stage<kW2, true, true, 2, AT, BT, AKC, BKC>(L, s + 2, lane, wm, wn, a, b, acc);
+    f8_stage<kW2, true, true, 3, AT, BT, AKC, BKC>(L, s + 3, lane, wm, wn, a, b, acc);
   }
-  f8_stage<kW2, true, false, 0, AT, BT, AKC, BKC>(t, s, i0, j0, wave, lane, wm, wn, a, b, acc);
-  f8_stage<kW1, true, false, 1, AT, BT, AKC, BKC>(t, s + 1, i0, j0, wave, lane, wm, wn, a, b, acc);
-  f8_stage<0, true, false, 2, AT, BT, AKC, BKC>(t, s + 2, i0, j0, wave, lane, wm, wn, a, b, acc);
-  f8_stage<0, false, false, 3, AT, BT, AKC, BKC>(t, s + 3, i0, j0, wave, lane, wm, wn, a, b, acc);
+  f8_stage<kW2, true, false, 0, AT, BT, AKC, BKC>(L, s, lane, wm, wn, a, b, acc);
+  f8_stage<kW1, true, false, 1, AT, BT, AKC, BKC>(L, s + 1, lane, wm, wn, a, b, acc);
+  f8_stage<0, true, false, 2, AT, BT, AKC, BKC>(L, s + 2, lane, wm, wn, a, b, acc);
+  f8_stage<0, false, false, 3, AT, BT, AKC, BKC>(L, s + 3, lane, wm, wn, a, b, acc);
 
   const float mx = tile_epilogue<DT>(t, e, acc, i0, j0, wm, wn, lane, tid, simple, vec);
   if (e.amax) amax_commit_block(e.amax, mx, red);

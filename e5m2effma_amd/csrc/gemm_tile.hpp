@@ -102,6 +102,26 @@ __device__ __forceinline__ void load_lds16(const uint8_t *src, const uint8_t *ld
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(l) : "memory", "m0");
 }
 
+// LDS byte address of p (a pointer into one of the ring buffers)
+__device__ __forceinline__ uint32_t lds_addr(const uint8_t *p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t *)p;
+}
+
+// p (wave-uniform) in scalar registers.  Values derived from the block index can be computed in vector
+// registers (integer division is), and an "s" asm operand is not moved to scalar registers by itself.
+__device__ __forceinline__ const uint8_t *uniform_ptr(const uint8_t *p) {
+  const uint64_t v = (uint64_t)(uintptr_t)p;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v), hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return (const uint8_t *)(uintptr_t)(((uint64_t)hi << 32) | lo);
+}
+
+// The same load with a wave-uniform 64-bit base in scalar registers and a 32-bit per-lane offset
+// (global_load_lds_dwordx4's saddr form: address = base + off); lds is the LDS byte address.  A loop
+// that keeps each lane's offsets fixed and advances only the base issues no vector address arithmetic.
+__device__ __forceinline__ void load_lds16s(const uint8_t *base, uint32_t off, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(lds) : "memory", "m0");
+}
+
 // Four consecutive elements of dtype T at element idx (4-element aligned) as FP32 (FP8 times sinv; the
 // others exact): one vector load
 template <int T> __device__ __forceinline__ void load4_t(const void *p, size_t idx, float sinv, float (&o)[4]) {
