@@ -6,7 +6,7 @@
 namespace e5ma {
 
 namespace {
-constexpr int kRound = 256;  // the K loop runs whole rounds of the 4-slot ring of 64-byte stages
+constexpr int kRound = 256;  // the K loop runs whole rings (4 x 64 or 2 x 128 K bytes)
 }
 
 bool gemm_f8_applies(int at, int bt, bool akc, bool bkc, int m, int n, int k, long long lda, long long ldb) {

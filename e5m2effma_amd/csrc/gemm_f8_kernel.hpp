@@ -6,23 +6,36 @@
 // translation unit per layout pair (gemm_f8_tn/nn/nt/tt.hip), which build in parallel.
 //
 // Block tile 256 x 256, 4 waves (one per SIMD), each owning a 128 x 128 sub-tile held as 4 x 4
-// accumulator blocks of v_mfma_f32_32x32x64_f8f6f4 (256 accumulator registers per lane).
-// K advances in stages of 64 bytes.  A 4-slot LDS ring (4 x 32 KiB, one object per slot and operand)
-// is filled by direct-to-LDS loads (global_load_lds_dwordx4: 64 lanes x 16 bytes land contiguously,
-// no VGPR staging) issued three stages ahead; each stage costs one barrier.  The loads address a stage
-// as a scalar base (advanced per stage) plus per-lane offsets fixed for the whole K loop, so the loop
-// issues no vector ALU instructions besides the MFMAs.  The fragments are
-// single-buffered (64 VGPRs beside the 256 accumulator registers) and the stage loop is unrolled by 4
-// so that ring slots are compile-time indices.  Within a stage the MFMAs, the fragment reads of the
-// next stage and the loads of stage s + 4 are interleaved.
+// accumulator blocks of v_mfma_f32_32x32x64_f8f6f4 (256 accumulator registers per lane).  K advances in
+// units of 64 bytes (one MFMA K step: 16 MFMAs per wave); during each unit the next unit's fragments
+// are read from LDS (double-buffered by unit parity, in the order its MFMAs use them).  The 128 KiB
+// LDS ring is filled by direct-to-LDS loads (global_load_lds_dwordx4: 64 lanes x 16 bytes land
+// contiguously, no VGPR staging) that address a stage as a scalar base (advanced per stage) plus
+// per-lane offsets fixed for the whole K loop, so the loop issues no vector ALU instructions besides
+// the MFMAs.  Two ring shapes (Ring<PAIR>), chosen by B's layout from measurements at 8192^3:
+// - PAIR (B K-contiguous): 2 stages of 128 K bytes (2 x 64 KiB), two units each.  A K-contiguous
+//   operand's rows are loaded 128 bytes (a whole cache line) per row and instruction: with 64-byte
+//   stages every line was requested twice, half each time, which cost 11% of the TN GEMM's time.  One
+//   barrier per stage, at its second unit: s_waitcnt vmcnt(0) lgkmcnt(0) completes this wave's loads
+//   of stage p + 1 and its reads of stage p's region (the second unit's fragments, read during the
+//   first), s_barrier makes both hold for every wave; then, during the second unit, stage p + 2's
+//   loads go into that region, one pair (A, B) after every second MFMA.
+// - 4 slots (B N-contiguous, whose rows are 256-byte k-rows either way): 4 stages of 64 K bytes, one
+//   unit each, one barrier per unit.  Stage s + 3's loads go into slot (s + 3) % 4 = (s - 1) % 4, whose
+//   last reads (stage s - 1's fragments) were issued during stage s - 2; the barrier starting stage s
+//   waits with lgkmcnt(15), which completes those but not the ones of stage s - 1, issued just before.
+//   One load pair goes out after every fourth MFMA.
+// Either way a stage's loads have two units of MFMAs to land.
 //
-// LDS layout of one operand stage (16 KiB), by source layout:
-// - K-contiguous: 256 rows (m or n) of 64 K bytes; 16-byte chunk c of row r is stored at chunk
-//   c ^ ((r >> 2) & 3).  gfx950's LDS serves a ds_read_b128 16 lanes per cycle over 64 banks
-//   (measured: a contiguous read takes 4 cycles, lanes l and l + 8 share a cycle, l and l + 16 do
-//   not); with this swizzle the fragment reads (2 x ds_read_b128 per lane) are conflict-free (measured).
-// - M / N-contiguous: 64 K rows of 256 m (or n) bytes, as the global rows are; chunk c of k-row kk is
-//   stored at chunk c ^ ((kk & 7) << 1).  Fragments are read with the transposing ds_read_b64_tr_b8
+// LDS layout of one operand stage, by source layout:
+// - K-contiguous: 256 rows (m or n) of kStageK K bytes; 16-byte chunk c of row r is stored at chunk
+//   c ^ swz(r) (swz(r) = (r >> 1) & 7 for 128-byte rows, (r >> 2) & 3 for 64-byte rows).  gfx950's LDS
+//   serves a ds_read_b128 16 lanes per cycle over 64 banks (measured: a contiguous read takes 4
+//   cycles, lanes l and l + 8 share a cycle, l and l + 16 do not).  A fragment read has 16 consecutive
+//   rows per cycle at one K chunk c; with 128-byte rows, rows 2u + v land on bank chunk 8v + (c ^ u),
+//   with 64-byte rows rows 4v + w on 4w + (c ^ v): all 16 distinct, so the reads are conflict-free.
+// - M / N-contiguous: kStageK K rows of 256 m (or n) bytes, as the global rows are; chunk c of k-row kk
+//   is stored at chunk c ^ ((kk & 7) << 1).  Fragments are read with the transposing ds_read_b64_tr_b8
 //   (4 per lane): within each group of 16 lanes, output lane 8h + t receives as its byte b the byte t
 //   of the 8 bytes addressed by lane 2b + h (measured on gfx950).  Lanes 2b + h address k-row b of an
 //   8-row group at rows (m) 8h..8h+7, so lane 8h + t gets 8 consecutive k of row 8h + t: the MFMA
@@ -39,26 +52,37 @@ namespace f8k {
 
 using namespace tile;
 
-constexpr int kBK = 64;                            // K bytes (= elements) per stage
-constexpr int kSlots = 4;                          // LDS ring depth (3 stages in flight)
-constexpr int kOpBytes = kBM * kBK;                // 16 KiB per operand and stage
-constexpr int kLoadsPerWave = kOpBytes / 1024 / 4; // dwordx4 LDS loads per wave, operand and stage
+constexpr int kUnitK = 64;  // K bytes (= elements) of one MFMA step
 
-__device__ __forceinline__ int swz(int r) { return (r >> 2) & 3; }
+template <bool PAIR> struct Ring {
+  static constexpr int kStageK = PAIR ? 128 : 64;          // K bytes per stage
+  static constexpr int kSlots = PAIR ? 2 : 4;              // stages the ring holds
+  static constexpr int kOpBytes = kBM * kStageK;           // per operand and stage
+  static constexpr int kLoads = kOpBytes / 1024 / 4;       // dwordx4 LDS loads per wave, operand and stage
+  static constexpr int kLanesPerRow = kStageK / 16;        // K-contiguous: lanes loading one row
+  static constexpr int kRowsPerLoad = 64 / kLanesPerRow;   // K-contiguous: rows per 1 KiB load
+  static constexpr int kW1 = 2 * kLoads;                   // one stage's loads of A and B, per wave
+  static_assert(kOpBytes * kSlots == 4 * kBufBytes, "the stages fill the ring");
+  __device__ static int swz(int r) { return PAIR ? (r >> 1) & 7 : (r >> 2) & 3; }
+  template <int S> __device__ static uint8_t *slot_a() { return lds_a<PAIR ? 2 * S : S>(); }
+  template <int S> __device__ static uint8_t *slot_b() { return lds_b<PAIR ? 2 * S : S>(); }
+};
 
 // Per-lane byte offset, from the operand's stage base, of this lane's 16 bytes in the 1 KiB
-// direct-to-LDS load blk (of 16) of an operand stage.  Stage s's base is P + r0 * ld + s * kBK for a
-// K-contiguous operand and P + r0 + s * kBK * ld for an M / N-contiguous one, so the offsets are the
-// same for every stage.
-// K-contiguous: rows r0 + 16 blk .. + 15, 64 K bytes each (rows past lim repeat row lim - 1); 16-byte
-// chunk c of row r lands at chunk c ^ swz(r).
+// direct-to-LDS load blk of an operand stage.  Stage p's base is P + r0 * ld + p * kStageK for a
+// K-contiguous operand and P + r0 + p * kStageK * ld for an M / N-contiguous one, so the offsets are
+// the same for every stage.
+// K-contiguous: rows r0 + kRowsPerLoad blk .., kStageK K bytes each (rows past lim repeat row lim - 1);
+// lane l fetches chunk (l % kLanesPerRow) ^ swz(r) of its row, which lands at chunk l % kLanesPerRow.
 // M / N-contiguous: k-rows 4 blk .. + 3 of the stage, 256 bytes of rows r0 .. r0 + 255 each (chunks
 // past lim, a multiple of 16, repeat the last chunk; never stored).
 // Offsets stay below 2^32 for ld <= kMaxLd (checked by the host).
-template <bool KC> __device__ __forceinline__ uint32_t op_offset(long long ld, int lim, int r0, int blk, int lane) {
+template <bool KC, bool PAIR>
+__device__ __forceinline__ uint32_t op_offset(long long ld, int lim, int r0, int blk, int lane) {
+  using G = Ring<PAIR>;
   if constexpr (KC) {
-    const int r = blk * 16 + (lane >> 2);
-    const int c = (lane & 3) ^ swz(r);
+    const int r = blk * G::kRowsPerLoad + lane / G::kLanesPerRow;
+    const int c = (lane % G::kLanesPerRow) ^ G::swz(r);
     return (uint32_t)(min(r0 + r, lim - 1) - r0) * (uint32_t)ld + 16 * c;
   } else {
     const int kk = blk * 4 + (lane >> 4);
@@ -68,59 +92,61 @@ template <bool KC> __device__ __forceinline__ uint32_t op_offset(long long ld, i
 }
 
 // What the loads of one block need: the operands' stage-0 bases and per-stage strides (wave-uniform)
-// and this lane's offsets for its share (kLoadsPerWave loads per operand and stage)
-struct Loads {
+// and this lane's offsets for its share (kLoads loads per operand and stage)
+template <bool PAIR> struct Loads {
   const uint8_t *a, *b;
   long long sa, sb;
-  uint32_t oa[kLoadsPerWave], ob[kLoadsPerWave];
-  uint32_t lds0;  // LDS offset of this wave's share within a buffer
+  uint32_t oa[Ring<PAIR>::kLoads], ob[Ring<PAIR>::kLoads];
+  uint32_t lds0;  // LDS offset of this wave's share within a stage
 };
 
-template <bool AKC, bool BKC>
-__device__ __forceinline__ Loads make_loads(const TileArgs &t, int i0, int j0, int wave, int lane) {
-  Loads L;
+template <bool AKC, bool BKC, bool PAIR>
+__device__ __forceinline__ Loads<PAIR> make_loads(const TileArgs &t, int i0, int j0, int wave, int lane) {
+  using G = Ring<PAIR>;
+  Loads<PAIR> L;
   L.a = uniform_ptr(t.A + (AKC ? (long long)i0 * t.lda : i0));
   L.b = uniform_ptr(t.B + (BKC ? (long long)j0 * t.ldb : j0));
-  L.sa = AKC ? kBK : kBK * t.lda;
-  L.sb = BKC ? kBK : kBK * t.ldb;
+  L.sa = AKC ? G::kStageK : G::kStageK * t.lda;
+  L.sb = BKC ? G::kStageK : G::kStageK * t.ldb;
 #pragma unroll
-  for (int q = 0; q < kLoadsPerWave; ++q) {
-    L.oa[q] = op_offset<AKC>(t.lda, t.m, i0, wave * kLoadsPerWave + q, lane);
-    L.ob[q] = op_offset<BKC>(t.ldb, t.n, j0, wave * kLoadsPerWave + q, lane);
+  for (int q = 0; q < G::kLoads; ++q) {
+    L.oa[q] = op_offset<AKC, PAIR>(t.lda, t.m, i0, wave * G::kLoads + q, lane);
+    L.ob[q] = op_offset<BKC, PAIR>(t.ldb, t.n, j0, wave * G::kLoads + q, lane);
   }
-  L.lds0 = wave * kLoadsPerWave * 1024;
+  L.lds0 = wave * G::kLoads * 1024;
   return L;
 }
 
-// load q (of kLoadsPerWave) of this wave's share of stage s: 1 KiB of A and 1 KiB of B into LDS
-// slot SLOT
-template <int SLOT>
-__device__ __forceinline__ void issue_load(const Loads &L, int s, int q) {
-  load_lds16s(L.a + s * L.sa, L.oa[q], lds_addr(lds_a<SLOT>()) + L.lds0 + q * 1024);
-  load_lds16s(L.b + s * L.sb, L.ob[q], lds_addr(lds_b<SLOT>()) + L.lds0 + q * 1024);
+// load q of this wave's share of stage p: 1 KiB of A and 1 KiB of B into ring slot S
+template <int S, bool PAIR>
+__device__ __forceinline__ void issue_load(const Loads<PAIR> &L, int p, int q) {
+  using G = Ring<PAIR>;
+  load_lds16s(L.a + p * L.sa, L.oa[q], lds_addr(G::template slot_a<S>()) + L.lds0 + q * 1024);
+  load_lds16s(L.b + p * L.sb, L.ob[q], lds_addr(G::template slot_b<S>()) + L.lds0 + q * 1024);
 }
-template <int SLOT>
-__device__ __forceinline__ void issue_stage(const Loads &L, int s) {
+template <int S, bool PAIR>
+__device__ __forceinline__ void issue_stage(const Loads<PAIR> &L, int p) {
 #pragma unroll
-  for (int q = 0; q < kLoadsPerWave; ++q) issue_load<SLOT>(L, s, q);
+  for (int q = 0; q < Ring<PAIR>::kLoads; ++q) issue_load<S, PAIR>(L, p, q);
 }
 
-// fragments of one 32-row block of an operand stage: lane l holds the 32 K bytes
-// [32 * (l / 32), + 32) of row r0 + l % 32 (r0 a multiple of 32)
-template <bool KC> __device__ __forceinline__ v8i read_frag(const uint8_t *s, int r0, int lane) {
+// fragments of one 32-row block of unit J of an operand stage: lane l holds the 32 K bytes
+// [64 J + 32 * (l / 32), + 32) of row r0 + l % 32 (r0 a multiple of 32)
+template <bool KC, bool PAIR, int J> __device__ __forceinline__ v8i read_frag(const uint8_t *s, int r0, int lane) {
+  using G = Ring<PAIR>;
   if constexpr (KC) {
     const int r = r0 + (lane & 31);
-    const int c0 = 2 * (lane >> 5);
-    const uint8_t *row = s + r * kBK;
-    const uint4 lo = *(const uint4 *)(row + 16 * (c0 ^ swz(r)));
-    const uint4 hi = *(const uint4 *)(row + 16 * ((c0 + 1) ^ swz(r)));
+    const int c0 = 4 * J + 2 * (lane >> 5);
+    const uint8_t *row = s + r * G::kStageK;
+    const uint4 lo = *(const uint4 *)(row + 16 * (c0 ^ G::swz(r)));
+    const uint4 hi = *(const uint4 *)(row + 16 * ((c0 + 1) ^ G::swz(r)));
     return v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
   } else {
-    // this lane addresses k-row 32 (g / 2) + 8 q + b, rows r .. r + 7 (r = r0 + 16 (g % 2) + 8 h) for
-    // read q; it receives row r0 + l % 32, k 32 (l / 32) + 8 q .. + 7
+    // this lane addresses k-row 64 J + 32 (g / 2) + 8 q + b, rows r .. r + 7 (r = r0 + 16 (g % 2) + 8 h)
+    // for read q; it receives row r0 + l % 32, k 64 J + 32 (l / 32) + 8 q .. + 7
     const int g = lane >> 4, h = lane & 1, b = (lane & 15) >> 1;
     const int r = r0 + 16 * (g & 1) + 8 * h;
-    const uint8_t *p = s + (32 * (g >> 1) + b) * kBM + 16 * ((r >> 4) ^ (b << 1)) + (r & 15);
+    const uint8_t *p = s + (kUnitK * J + 32 * (g >> 1) + b) * kBM + 16 * ((r >> 4) ^ (b << 1)) + (r & 15);
     const v2i q0 = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i *)(p + 0 * 8 * kBM));
     const v2i q1 = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i *)(p + 1 * 8 * kBM));
     const v2i q2 = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i *)(p + 2 * 8 * kBM));
@@ -129,20 +155,20 @@ template <bool KC> __device__ __forceinline__ v8i read_frag(const uint8_t *s, in
   }
 }
 
-// Stage s (= SLOT mod 4) of the K loop.  The fragments are double-buffered by stage parity: set
-// P = SLOT & 1 holds stage s's, and stage s + 1's are read into set 1 - P from the start of stage s, one
-// fragment every second MFMA (LDS reads interleaved one per MFMA), so they have the whole stage to
-// land.  (Single-buffered, the last reads of a stage were issued with its last MFMAs; slowed by the
-// direct-to-LDS writes, they left the matrix cores idle at the barrier.)  WAITN: global loads this wave
-// may leave in flight when stage s + 1 must have landed; NEXT: a stage s + 1 exists; ISSUE: stage s + 4
-// exists.  The loads of stage s + 4 into stage s's slot (free: every wave read it before the barrier)
-// go out one pair after every fourth MFMA.  (Issuing the 8 loads as one burst stalled the MFMA stream.)
-template <int WAITN, bool NEXT, bool ISSUE, int SLOT, int AT, int BT, bool AKC, bool BKC>
-__device__ __forceinline__ void f8_stage(const Loads &L, int s, int lane, int wm, int wn, v8i (&a)[2][4],
-                                         v8i (&b)[2][4], v16f (&acc)[4][4]) {
-  constexpr int P = SLOT & 1, Q = P ^ 1;
-  if constexpr (NEXT) wait_barrier<WAITN>();
-  const uint8_t *na = lds_a<(SLOT + 1) & 3>(), *nb = lds_b<(SLOT + 1) & 3>();
+// One unit: 16 MFMAs on fragment set P.
+// BAR: starts with wait_barrier<WAITN, LGK>.
+// NEXT: the next unit's fragments (ring slot NS, unit NJ of that stage) are read into set 1 - P, one
+//   every second MFMA in the order its MFMAs use them (its first four need a0 and all of b): a0, b0,
+//   b1, b2, b3, a1, a2, a3.
+// ISSUE: stage ls's loads go into ring slot IS, one pair (A, B) after every (16 / kLoads)-th MFMA.
+template <bool PAIR, int P, bool BAR, int WAITN, int LGK, bool NEXT, int NS, int NJ, bool ISSUE, int IS, int AT,
+          int BT, bool AKC, bool BKC>
+__device__ __forceinline__ void f8_unit(const Loads<PAIR> &L, int ls, int lane, int wm, int wn, v8i (&a)[2][4],
+                                        v8i (&b)[2][4], v16f (&acc)[4][4]) {
+  using G = Ring<PAIR>;
+  constexpr int Q = 1 - P, kEvery = 16 / G::kLoads;
+  if constexpr (BAR) wait_barrier<WAITN, LGK>();
+  const uint8_t *na = G::template slot_a<NS>(), *nb = G::template slot_b<NS>();
 #pragma unroll
   for (int x = 0; x < 4; ++x) {
 #pragma unroll
@@ -151,15 +177,18 @@ __device__ __forceinline__ void f8_stage(const Loads &L, int s, int lane, int wm
       // with the neutral scale 127, one instruction dword pair shorter)
       acc[x][y] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a[P][x], b[P][y], acc[x][y], kMfmaFmt<AT>,
                                                                   kMfmaFmt<BT>, 0, 0, 0, 0);
+      const int i = 4 * x + y;
       if constexpr (ISSUE) {
-        if (y == 1) issue_load<SLOT>(L, s + 4, x);
+        if (i % kEvery == 1) issue_load<IS, PAIR>(L, ls, i / kEvery);
       }
       if constexpr (NEXT) {
-        const int i = 4 * x + y;  // fragment i / 2 of the next stage after MFMA i (i even)
         if ((i & 1) == 0) {
           const int f = i >> 1;
-          if (f < 4) a[Q][f] = read_frag<AKC>(na, 128 * wm + 32 * f, lane);
-          else b[Q][f - 4] = read_frag<BKC>(nb, 128 * wn + 32 * (f - 4), lane);
+          if (f >= 1 && f <= 4) b[Q][f - 1] = read_frag<BKC, PAIR, NJ>(nb, 128 * wn + 32 * (f - 1), lane);
+          else {
+            const int fa = f == 0 ? 0 : f - 4;
+            a[Q][fa] = read_frag<AKC, PAIR, NJ>(na, 128 * wm + 32 * fa, lane);
+          }
         }
       }
     }
@@ -174,8 +203,69 @@ __device__ __forceinline__ void f8_stage(const Loads &L, int s, int lane, int wm
   }
 }
 
+// The K loop of one block (nk units of 64 K) with the 4-slot ring: unit s is stage s in slot s % 4
+template <int AT, int BT, bool AKC, bool BKC>
+__device__ __forceinline__ void k_loop(const Loads<false> &L, int nk, int lane, int wm, int wn, v8i (&a)[2][4],
+                                       v8i (&b)[2][4], v16f (&acc)[4][4]) {
+  constexpr int W = Ring<false>::kW1;
+  // stages 0..2 in flight; stage 0's fragments once it has landed
+  issue_stage<0, false>(L, 0);
+  issue_stage<1, false>(L, 1);
+  issue_stage<2, false>(L, 2);
+  wait_barrier<2 * W>();
+#pragma unroll
+  for (int x = 0; x < 4; ++x) {
+    a[0][x] = read_frag<AKC, false, 0>(lds_a<0>(), 128 * wm + 32 * x, lane);
+    b[0][x] = read_frag<BKC, false, 0>(lds_b<0>(), 128 * wn + 32 * x, lane);
+  }
+  // four stages per iteration, each awaiting s + 1 (s + 2 in flight) and issuing s + 3; then the last
+  // four drain the ring (nk % 4 == 0, nk >= 8)
+  int s = 0;
+  for (; s < nk - 4; s += 4) {
+    f8_unit<false, 0, true, W, 15, true, 1, 0, true, 3, AT, BT, AKC, BKC>(L, s + 3, lane, wm, wn, a, b, acc);
+    f8_unit<false, 1, true, W, 15, true, 2, 0, true, 0, AT, BT, AKC, BKC>(L, s + 4, lane, wm, wn, a, b, acc);
+    f8_unit<false, 0, true, W, 15, true, 3, 0, true, 1, AT, BT, AKC, BKC>(L, s + 5, lane, wm, wn, a, b, acc);
+    f8_unit<false, 1, true, W, 15, true, 0, 0, true, 2, AT, BT, AKC, BKC>(L, s + 6, lane, wm, wn, a, b, acc);
+  }
+  f8_unit<false, 0, true, W, 15, true, 1, 0, true, 3, AT, BT, AKC, BKC>(L, s + 3, lane, wm, wn, a, b, acc);
+  f8_unit<false, 1, true, W, 15, true, 2, 0, false, 0, AT, BT, AKC, BKC>(L, 0, lane, wm, wn, a, b, acc);
+  f8_unit<false, 0, true, 0, 15, true, 3, 0, false, 0, AT, BT, AKC, BKC>(L, 0, lane, wm, wn, a, b, acc);
+  f8_unit<false, 1, false, 0, 0, false, 0, 0, false, 0, AT, BT, AKC, BKC>(L, 0, lane, wm, wn, a, b, acc);
+}
+
+// The K loop with the 2-stage ring: stage p (units 2p, 2p + 1) in region p % 2
+template <int AT, int BT, bool AKC, bool BKC>
+__device__ __forceinline__ void k_loop(const Loads<true> &L, int nk, int lane, int wm, int wn, v8i (&a)[2][4],
+                                       v8i (&b)[2][4], v16f (&acc)[4][4]) {
+  constexpr int W = Ring<true>::kW1;
+  const int np = nk / 2;  // stages: even, >= 4
+  // stages 0 and 1 in flight; stage 0's first-unit fragments once it has landed
+  issue_stage<0, true>(L, 0);
+  issue_stage<1, true>(L, 1);
+  wait_barrier<W>();
+#pragma unroll
+  for (int x = 0; x < 4; ++x) {
+    a[0][x] = read_frag<AKC, true, 0>(lds_a<0>(), 128 * wm + 32 * x, lane);
+    b[0][x] = read_frag<BKC, true, 0>(lds_b<0>(), 128 * wn + 32 * x, lane);
+  }
+  // two stages (one per region) per iteration, each issuing stage p + 2 in its second unit; then the
+  // last two stages
+  int p = 0;
+  for (; p < np - 2; p += 2) {
+    f8_unit<true, 0, false, 0, 0, true, 0, 1, false, 0, AT, BT, AKC, BKC>(L, 0, lane, wm, wn, a, b, acc);
+    f8_unit<true, 1, true, 0, 0, true, 1, 0, true, 0, AT, BT, AKC, BKC>(L, p + 2, lane, wm, wn, a, b, acc);
+    f8_unit<true, 0, false, 0, 0, true, 1, 1, false, 0, AT, BT, AKC, BKC>(L, 0, lane, wm, wn, a, b, acc);
+    f8_unit<true, 1, true, 0, 0, true, 0, 0, true, 1, AT, BT, AKC, BKC>(L, p + 3, lane, wm, wn, a, b, acc);
+  }
+  f8_unit<true, 0, false, 0, 0, true, 0, 1, false, 0, AT, BT, AKC, BKC>(L, 0, lane, wm, wn, a, b, acc);
+  f8_unit<true, 1, true, 0, 0, true, 1, 0, false, 0, AT, BT, AKC, BKC>(L, 0, lane, wm, wn, a, b, acc);
+  f8_unit<true, 0, false, 0, 0, true, 1, 1, false, 0, AT, BT, AKC, BKC>(L, 0, lane, wm, wn, a, b, acc);
+  f8_unit<true, 1, false, 0, 0, false, 0, 0, false, 0, AT, BT, AKC, BKC>(L, 0, lane, wm, wn, a, b, acc);
+}
+
 template <int AT, int BT, int DT, bool AKC, bool BKC>
 __global__ __launch_bounds__(kThreads, 1) void gemm_f8_kernel(TileArgs t, Epilogue e, int simple, int vec) {
+  constexpr bool PAIR = BKC;  // the ring shape measured faster for this layout
   __shared__ float red[kThreads / 64];
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
@@ -183,7 +273,6 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_f8_kernel(TileArgs t, Epilog
   tile_of(blockIdx.x, t, tm, tn, sp);
   apply_split(t, e, sp);
   const int i0 = tm * kBM, j0 = tn * kBN;
-  const int nk = t.k / kBK;
 
   v16f acc[4][4];
 #pragma unroll
@@ -192,34 +281,9 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_f8_kernel(TileArgs t, Epilog
     for (int y = 0; y < 4; ++y)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[x][y][r] = 0.f;
-
-  // prologue: stages 0..2 in flight; stage 3 is issued once every wave is past the first barrier
-  const Loads L = make_loads<AKC, BKC>(t, i0, j0, wave, lane);
-  issue_stage<0>(L, 0);
-  issue_stage<1>(L, 1);
-  issue_stage<2>(L, 2);
-  wait_barrier<2 * 2 * kLoadsPerWave>();  // stage 0 landed; stages 1 and 2 may be in flight
-  issue_stage<3>(L, 3);
-  v8i a[2][4], b[2][4];  // fragments, double-buffered by stage parity
-#pragma unroll
-  for (int x = 0; x < 4; ++x) {
-    a[0][x] = read_frag<AKC>(lds_a<0>(), 128 * wm + 32 * x, lane);
-    b[0][x] = read_frag<BKC>(lds_b<0>(), 128 * wn + 32 * x, lane);
-  }
-  // steady state, four stages (one per ring slot) per iteration: stages s + 2 and s + 3 in flight
-  // while s + 1 is awaited; then the last four stages drain the ring (nk % 4 == 0)
-  constexpr int kW2 = 2 * 2 * kLoadsPerWave, kW1 = 2 * kLoadsPerWave;
-  int s = 0;
-  for (; s < nk - 4; s += 4) {
-    f8_stage<kW2, true, true, 0, AT, BT, AKC, BKC>(L, s, lane, wm, wn, a, b, acc);
-    f8_stage<kW2, true, true, 1, AT, BT, AKC, BKC>(L, s + 1, lane, wm, wn, a, b, acc);
-    f8_stage<kW2, true, true, 2, AT, BT, AKC, BKC>(L, s + 2, lane, wm, wn, a, b, acc);
-    f8_stage<kW2, true, true, 3, AT, BT, AKC, BKC>(L, s + 3, lane, wm, wn, a, b, acc);
-  }
-  f8_stage<kW2, true, false, 0, AT, BT, AKC, BKC>(L, s, lane, wm, wn, a, b, acc);
-  f8_stage<kW1, true, false, 1, AT, BT, AKC, BKC>(L, s + 1, lane, wm, wn, a, b, acc);
-  f8_stage<0, true, false, 2, AT, BT, AKC, BKC>(L, s + 2, lane, wm, wn, a, b, acc);
-  f8_stage<0, false, false, 3, AT, BT, AKC, BKC>(L, s + 3, lane, wm, wn, a, b, acc);
+  v8i a[2][4], b[2][4];  // fragments, double-buffered by unit parity
+  const Loads<PAIR> L = make_loads<AKC, BKC, PAIR>(t, i0, j0, wave, lane);
+  k_loop<AT, BT, AKC, BKC>(L, t.k / kUnitK, lane, wm, wn, a, b, acc);
 
   const float mx = tile_epilogue<DT>(t, e, acc, i0, j0, wm, wn, lane, tid, simple, vec);
   if (e.amax) amax_commit_block(e.amax, mx, red);

@@ -18,18 +18,13 @@ constexpr int kGroupM = 4;        // tile order: groups of 4 m-tiles
 
 typedef __attribute__((address_space(3))) v2i lds_v2i;
 
-// The LDS ring: 8 buffers of 16 KiB (4 slots x 2 operands in the K loop; 8 column groups in the
-// epilogue), each its own object, addressed with compile-time indices.
-__shared__ __attribute__((aligned(1024))) uint8_t g_sa0[kBufBytes], g_sa1[kBufBytes], g_sa2[kBufBytes], g_sa3[kBufBytes];
-__shared__ __attribute__((aligned(1024))) uint8_t g_sb0[kBufBytes], g_sb1[kBufBytes], g_sb2[kBufBytes], g_sb3[kBufBytes];
-template <int S> __device__ __forceinline__ uint8_t *lds_a() {
-  if constexpr (S == 0) return g_sa0; else if constexpr (S == 1) return g_sa1; else if constexpr (S == 2) return g_sa2;
-  else return g_sa3;
-}
-template <int S> __device__ __forceinline__ uint8_t *lds_b() {
-  if constexpr (S == 0) return g_sb0; else if constexpr (S == 1) return g_sb1; else if constexpr (S == 2) return g_sb2;
-  else return g_sb3;
-}
+// The LDS ring: 128 KiB as two 32 KiB regions per operand, each its own object.  The FP8 kernel uses
+// each region as one 128-byte K stage of an operand; the BF16-matrix-core kernel and the epilogue use
+// the 8 halves (16 KiB buffers: 4 slots x 2 operands, or 8 column groups) with compile-time indices.
+__shared__ __attribute__((aligned(1024))) uint8_t g_ra0[2 * kBufBytes], g_ra1[2 * kBufBytes];
+__shared__ __attribute__((aligned(1024))) uint8_t g_rb0[2 * kBufBytes], g_rb1[2 * kBufBytes];
+template <int S> __device__ __forceinline__ uint8_t *lds_a() { return (S < 2 ? g_ra0 : g_ra1) + (S & 1) * kBufBytes; }
+template <int S> __device__ __forceinline__ uint8_t *lds_b() { return (S < 2 ? g_rb0 : g_rb1) + (S & 1) * kBufBytes; }
 // the ring's 8 buffers as the epilogue's 8 column groups of 16 FP32 columns x 256 rows (g is
 // wave-uniform, or a constant after unrolling)
 __device__ __forceinline__ float *stage_at(int g) {
@@ -50,10 +45,12 @@ __device__ __forceinline__ float acc_read(float a) {
   return v;
 }
 
-// s_waitcnt vmcnt(N) lgkmcnt(0), then s_barrier; the memory clobber keeps the compiler from moving
+// s_waitcnt vmcnt(N) lgkmcnt(LGK), then s_barrier; the memory clobber keeps the compiler from moving
 // memory operations across it.  (__syncthreads would also wait for every outstanding global load.)
-template <int N> __device__ __forceinline__ void wait_barrier() {
-  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+// LDS reads complete in issue order, so lgkmcnt(LGK) leaves at most the LGK latest reads (and scalar
+// loads) in flight.
+template <int N, int LGK = 0> __device__ __forceinline__ void wait_barrier() {
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(%1)\n\ts_barrier" ::"n"(N), "n"(LGK) : "memory");
 }
 
 struct TileArgs {
@@ -118,8 +115,12 @@ __device__ __forceinline__ const uint8_t *uniform_ptr(const uint8_t *p) {
 // The same load with a wave-uniform 64-bit base in scalar registers and a 32-bit per-lane offset
 // (global_load_lds_dwordx4's saddr form: address = base + off); lds is the LDS byte address.  A loop
 // that keeps each lane's offsets fixed and advances only the base issues no vector address arithmetic.
+// Both scalar operands go through uniform_ptr / readfirstlane (a no-op for values already in scalar
+// registers), since register pressure can leave a hoisted uniform value in a vector register.
 __device__ __forceinline__ void load_lds16s(const uint8_t *base, uint32_t off, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(lds) : "memory", "m0");
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(uniform_ptr(base)),
+               "s"(__builtin_amdgcn_readfirstlane(lds))
+               : "memory", "m0");
 }
 
 // Four consecutive elements of dtype T at element idx (4-element aligned) as FP32 (FP8 times sinv; the
