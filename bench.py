@@ -315,6 +315,29 @@ def main():
         secondary.append({"workload": "cast 8192x8192 FP32 -> E5M2 (scale, amax)", "id": "cast_8192sq_fp32_e5m2",
                           "value": round(gbs, 1), "unit": "GB/s", "ms_per_call": round(ms, 5), "bytes_per_call": nbytes,
                           "roofline": roof("hbm", gbs, HBM_PEAK_GBS, "GB/s", "cast_8192sq_fp32_e5m2")})
+
+        # Float8Tensor.from_float's quantization in one e5ma_quantize call: per tensor, an amax pass then
+        # the scaled cast (4 + 4 + 1 bytes per element); per row, each 8192-element row read once
+        # (4 + 1 bytes per element, plus scale_inv and amax per row)
+        qsc = torch.empty(8192, dtype=torch.float32, device=dev)
+        qam = torch.empty(8192, dtype=torch.float32, device=dev)
+        for wid, fmt, per_row, what in (
+                ("quantize_8192sq_fp32_e5m2_tensor", E5M2, False, "per tensor: amax pass + scaled cast"),
+                ("quantize_8192sq_fp32_e4m3_rows", E4M3, True, "per row, rows read once")):
+            Dq = _lib.tensor(dst.data_ptr(), fmt, scaling=_lib.SCALING_OUTER if per_row else _lib.SCALING_TENSOR)
+            rows, cols = (8192, 8192) if per_row else (1, n)
+
+            def f(i=0, Dq=Dq, rows=rows, cols=cols):
+                check(L.e5ma_quantize(ctypes.byref(descs[i % nbuf]), ctypes.byref(Dq), rows, cols,
+                                      57344.0 if fmt == E5M2 else 448.0, qsc.data_ptr(), qam.data_ptr(), sp),
+                      "quantize")
+            ms = timed(f, max(K, 20), W)
+            nbytes = n * 5 + 8192 * 8 if per_row else n * 9
+            gbs = nbytes / (ms * 1e-3) / 1e9
+            secondary.append({"workload": f"quantize 8192x8192 FP32 -> {'E4M3' if fmt == E4M3 else 'E5M2'} with "
+                                          f"scale from amax ({what})", "id": wid,
+                              "value": round(gbs, 1), "unit": "GB/s", "ms_per_call": round(ms, 5),
+                              "bytes_per_call": nbytes, "roofline": roof("hbm", gbs, HBM_PEAK_GBS, "GB/s", wid)})
         del srcs, dst
 
     # ---- device copy 1 GiB: the practical streaming ceiling and the counters' calibration kernel -----

@@ -7,6 +7,7 @@ functional interface of the reference's Python package (reference
 * ``matmul(a, b, ...)``: ``out = alpha * (scale_a * scale_b) * (a @ b) + bias + beta * out``;
 * ``linear(x, weight, bias, ...)``: ``x @ weight.t() + bias``;
 * ``cast(x, dtype, ...)``: element-wise conversion with scale_inv / scale / amax;
+* ``quantize(x, dtype, ...)``: FP8 codes with a scale from x's own amax, per tensor or per row;
 * ``adam_step(param, grad, exp_avg, exp_avg_sq, ...)``: one fused in-place Adam / AdamW step;
 * ``AdamW``: a ``torch.optim`` optimizer on that step (``optim.py``);
 * ``Float8Tensor`` / ``quantize_linear_``: FP8 weights with their scale that ``@``, ``F.linear`` and
@@ -35,7 +36,7 @@ e5m2 = torch.float8_e5m2
 e4m3 = torch.float8_e4m3fn
 if not hasattr(torch, "e5m2effma"):
     torch.e5m2effma = e5m2
-__all__ = ["matmul", "linear", "cast", "adam_step", "AdamW", "Float8Tensor", "quantize_linear_", "gemm_raw", "e5m2",
+__all__ = ["matmul", "linear", "cast", "quantize", "adam_step", "AdamW", "Float8Tensor", "quantize_linear_", "gemm_raw", "e5m2",
            "e4m3", "__version__"]
 
 _CODE = {torch.float8_e4m3fn: E4M3, torch.bfloat16: BF16, torch.float16: FP16, torch.float32: FP32,
@@ -249,6 +250,42 @@ def cast(x: torch.Tensor, dtype: torch.dtype, *, scale_inv: Optional[torch.Tenso
         s = _lib.lib().e5ma_cast(ctypes.byref(S), ctypes.byref(D), xc.numel(), _stream())
     _check_status(s, "e5ma_cast")
     return y
+
+
+def quantize(x: torch.Tensor, dtype: torch.dtype = torch.float8_e5m2, *, per_row: bool = False, margin: float = 1.0,
+             scale_inv: Optional[torch.Tensor] = None):
+    """FP8 codes of ``x`` with a scale from its own amax, per tensor or per row of a 2-D ``x``, on
+    ``e5ma_quantize`` (include/e5m2effma_ext.h): the steps of the reference's
+    ``Float8Tensor.from_float`` (``tensor.py:60-74``) in one call.  ``scale = margin * max_finite / amax``
+    (amax clamped to 1e-12), codes RNE-satfinite of ``x * scale``.  Returns ``(codes, scale_inv, amax)``,
+    the last two float32 of shape (1,) or (rows,).  ``scale_inv`` dequantizes an FP8 ``x``."""
+    _check_gpu(x.device)
+    dev = x.device
+    st = _code(x.dtype, "x")
+    if dtype not in _FP8:
+        raise TypeError(f"dtype must be torch.float8_e5m2 or torch.float8_e4m3fn, got {dtype}")
+    if scale_inv is not None and x.dtype not in _FP8:
+        raise ValueError("scale_inv is only meaningful for an FP8 x")
+    if per_row and x.dim() != 2:
+        raise ValueError(f"per_row quantization needs a 2-D tensor, got shape {tuple(x.shape)}")
+    if not margin > 0:
+        raise ValueError(f"margin must be positive, got {margin}")
+    xc = x.contiguous()
+    rows, cols = (xc.shape[0], xc.shape[1]) if per_row else (1, xc.numel())
+    groups = rows if per_row else 1
+    codes = torch.empty(xc.shape, dtype=dtype, device=dev)
+    sinv = torch.empty(groups, dtype=torch.float32, device=dev)
+    amax = torch.empty(groups, dtype=torch.float32, device=dev)
+    qmax = float(torch.tensor(margin * (57344.0 if dtype == torch.float8_e5m2 else 448.0), dtype=torch.float32))
+    if xc.numel() == 0:
+        return codes, sinv.fill_(float("nan")), amax.zero_()
+    with torch.cuda.device(dev):
+        S = _lib.tensor(xc.data_ptr(), st, _scalar_ptr(scale_inv, dev, "scale_inv"))
+        D = _lib.tensor(codes.data_ptr(), _CODE[dtype], scaling=_lib.SCALING_OUTER if per_row else _lib.SCALING_TENSOR)
+        s = _lib.lib().e5ma_quantize(ctypes.byref(S), ctypes.byref(D), rows, cols, qmax, sinv.data_ptr(),
+                                     amax.data_ptr(), _stream())
+    _check_status(s, "e5ma_quantize")
+    return codes, sinv, amax
 
 
 def adam_step(param: torch.Tensor, grad: torch.Tensor, exp_avg: torch.Tensor, exp_avg_sq: torch.Tensor, *,

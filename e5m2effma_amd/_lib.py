@@ -1,4 +1,5 @@
-"""ctypes binding of the C ABI in ``include/e5m2effma.h`` (``libe5m2effma.so``, built in-tree).
+"""ctypes binding of the C ABI in ``include/e5m2effma.h`` and ``include/e5m2effma_ext.h``
+(``libe5m2effma.so``, built in-tree).
 
 Loading fails loudly when the library is missing: there is no fallback path.
 """
@@ -13,8 +14,8 @@ OP_N, OP_T = 0, 1
 OK, INVALID_VALUE, NOT_SUPPORTED, HIP_ERROR = 0, 1, 2, 3
 SCALING_TENSOR, SCALING_OUTER = 0, 1
 
-# every symbol include/e5m2effma.h declares
-EXPORTS = ("e5ma_gemm", "e5ma_cast", "e5ma_adam", "e5ma_status_string", "e5ma_last_error")
+# every symbol include/e5m2effma.h and include/e5m2effma_ext.h declare
+EXPORTS = ("e5ma_gemm", "e5ma_cast", "e5ma_adam", "e5ma_status_string", "e5ma_last_error", "e5ma_quantize")
 
 
 class Tensor(ctypes.Structure):
@@ -47,6 +48,8 @@ def lib():
         L.e5ma_gemm.argtypes = [I, I, I, I, I, F, TP, I, TP, I, F, TP, I, TP, I, TP, P]
         L.e5ma_cast.restype = I
         L.e5ma_cast.argtypes = [TP, TP, S, P]
+        L.e5ma_quantize.restype = I
+        L.e5ma_quantize.argtypes = [TP, TP, S, S, F, P, P, P]
         L.e5ma_adam.restype = I
         L.e5ma_adam.argtypes = [ctypes.POINTER(AdamConfig), S, TP, TP, TP, TP, TP, P]
         L.e5ma_status_string.restype = ctypes.c_char_p

@@ -8,6 +8,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include "e5m2effma_ext.h"
 #include "e5ma_host.hpp"
 
 namespace e5ma {
@@ -109,6 +110,34 @@ extern "C" e5ma_status e5ma_cast(const e5ma_tensor *src, const e5ma_tensor *dst,
                                           is_fp8(src->dtype) ? src->scale_inv : nullptr,
                                           is_fp8(dst->dtype) ? dst->scale : nullptr, dst->amax, stream);
   return e5ma::hip_status(err, "e5ma_cast: kernel launch");
+}
+
+// No C-ABI counterpart in the reference: its Float8Tensor.from_float runs these steps as torch
+// operations plus e5ma_cast (binds/python/e5m2effma/tensor.py:60-74)
+extern "C" e5ma_status e5ma_quantize(const e5ma_tensor *src, const e5ma_tensor *dst, size_t rows, size_t cols,
+                                     float qmax, float *scale_inv, float *amax_out, hipStream_t stream) {
+  e5ma::clear_error();
+  if (!src || !dst || !src->data || !dst->data || !scale_inv)
+    return fail(E5MA_INVALID_VALUE, "e5ma_quantize: src / dst, their data or scale_inv is NULL");
+  if (!valid_dtype(src->dtype) || !is_fp8(dst->dtype))
+    return fail(E5MA_INVALID_VALUE, "e5ma_quantize: src dtype %d / dst dtype %d (dst must be E5MA_E4M3 or E5MA_E5M2)",
+                (int)src->dtype, (int)dst->dtype);
+  if (src->scaling != E5MA_SCALING_TENSOR)
+    return fail(E5MA_INVALID_VALUE, "e5ma_quantize: src takes per-tensor scaling only");
+  if (dst->scaling != E5MA_SCALING_TENSOR && dst->scaling != E5MA_SCALING_OUTER)
+    return fail(E5MA_INVALID_VALUE, "e5ma_quantize: invalid dst scaling %d", (int)dst->scaling);
+  if (!(qmax > 0.f) || isinf(qmax))
+    return fail(E5MA_INVALID_VALUE, "e5ma_quantize: qmax = %g must be positive and finite", (double)qmax);
+  if (rows == 0 || cols == 0) return E5MA_OK;
+  if (cols > SIZE_MAX / rows) return fail(E5MA_INVALID_VALUE, "e5ma_quantize: rows x cols overflows");
+  // per row, a launch has up to 256 threads per row and HIP's grid holds fewer than 2^32 threads
+  if (dst->scaling == E5MA_SCALING_OUTER && rows >= ((size_t)1 << 24))
+    return fail(E5MA_INVALID_VALUE, "e5ma_quantize: per-row scaling takes at most %d rows, got %zu", (1 << 24) - 1, rows);
+  if (e5ma_status st = e5ma::check_device()) return st;
+  const hipError_t err = e5ma::launch_quantize(src->dtype, dst->dtype, src->data, dst->data, rows, cols,
+                                               is_fp8(src->dtype) ? src->scale_inv : nullptr, qmax,
+                                               dst->scaling == E5MA_SCALING_OUTER, scale_inv, amax_out, stream);
+  return e5ma::hip_status(err, "e5ma_quantize: kernel launch");
 }
 
 // reference src/adamw_e5m2effma.cu:125-168

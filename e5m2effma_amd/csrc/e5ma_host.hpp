@@ -32,6 +32,10 @@ e5ma_status check_device(int *dev_out = nullptr);
 hipError_t launch_cast(int tin, int tout, const void *src, void *dst, size_t count, const float *sinv,
                        const float *qscale, float *amax, hipStream_t s);
 
+// Float8Tensor.from_float's quantization (include/e5m2effma_ext.h): per tensor (two passes) or per row.
+hipError_t launch_quantize(int tin, int tout, const void *src, void *dst, size_t rows, size_t cols, const float *sinv,
+                           float qmax, bool per_row, float *scale_inv, float *amax, hipStream_t s);
+
 struct AdamScalars {
   float lr, beta1, beta2, omb1, omb2, rbc1, rbc2, eps, lr_wd, wd, gscale;
   int adamw;

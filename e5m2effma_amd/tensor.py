@@ -52,25 +52,20 @@ class Float8Tensor(torch.Tensor):
     @classmethod
     def from_float(cls, x: torch.Tensor, *, fp8: torch.dtype = torch.float8_e5m2, per_row: bool = False,
                    dtype: Optional[torch.dtype] = None, margin: float = 1.0) -> "Float8Tensor":
-        """Quantize ``x`` with scale = margin * max_finite(fp8) / amax, per tensor (through ``e5ma_cast``)
-        or per row of a 2-D ``x``.  The nominal dtype defaults to ``x``'s (bfloat16 for other dtypes)."""
+        """Quantize ``x`` with scale = margin * max_finite(fp8) / amax, per tensor or per row of a 2-D ``x``,
+        in one ``e5ma_quantize`` call (the reference composes the same steps from torch operations and
+        e5ma_cast, tensor.py:60-74).  The nominal dtype defaults to ``x``'s (bfloat16 for other dtypes)."""
         if x.device.type != "cuda":
             raise ValueError("Float8Tensor.from_float needs a tensor on a ROCm device")
         if fp8 not in _FP8_MAX:
             raise TypeError(f"fp8 must be torch.float8_e5m2 or torch.float8_e4m3fn, got {fp8}")
         if dtype is None:
             dtype = x.dtype if x.dtype in _NOMINAL else torch.bfloat16
-        top = margin * _FP8_MAX[fp8]
-        xf = x.detach().float()
-        if per_row:
-            if x.dim() != 2:
-                raise ValueError(f"per_row quantization needs a 2-D tensor, got shape {tuple(x.shape)}")
-            scale = top / xf.abs().amax(dim=1).clamp_min(1e-12)
-            codes = (xf * scale[:, None]).clamp(-_FP8_MAX[fp8], _FP8_MAX[fp8]).to(fp8)
-            return cls(codes, (1.0 / scale).float(), 0, dtype)
-        from . import cast
-        scale = (top / xf.abs().amax().clamp_min(1e-12)).reshape(1).float()
-        return cls(cast(xf.contiguous(), fp8, scale=scale), 1.0 / scale, None, dtype)
+        if per_row and x.dim() != 2:
+            raise ValueError(f"per_row quantization needs a 2-D tensor, got shape {tuple(x.shape)}")
+        from . import quantize
+        codes, scale_inv, _ = quantize(x.detach(), fp8, per_row=per_row, margin=margin)
+        return cls(codes, scale_inv, 0 if per_row else None, dtype)
 
     def dequantize(self, dtype: Optional[torch.dtype] = None) -> torch.Tensor:
         s = self._scale_inv

@@ -77,6 +77,7 @@ def lib():
                 "orc_lane_sweep": (None, [vp, vp, sz, i, i, vp]),
                 "orc_encode_selfcheck": (sz, [i, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_uint64, vp]),
                 "orc_cast": (f, [i, i, vp, vp, sz, f, f, f]),
+                "orc_quantize": (None, [i, i, vp, vp, sz, sz, f, f, i, vp, vp]),
                 "orc_gemm_chain": (f, [vp, f, i, i, i]),
                 "orc_gemm_exact": (None, [vp, vp, vp, sz, vp, vp]),
                 "orc_gemm_check": (sz, [vp, vp, vp, vp, vp, sz, ctypes.c_double, vp, vp, vp]),
@@ -145,6 +146,18 @@ def cast(tin, tout, src, count, sinv=1.0, qscale=1.0, amax_in=0.0):
     dst = np.empty(count, dtype=NP_DTYPE[tout])
     amax = lib().orc_cast(tin, tout, _p(np.ascontiguousarray(src)), _p(dst), count, sinv, qscale, amax_in)
     return dst, amax
+
+
+def quantize(tin, tout, src, rows, cols, qmax, per_row=False, sinv=1.0):
+    """Float8Tensor.from_float's quantization of a rows x cols row-major ``src`` (codes of ``tin``):
+    returns (codes, scale_inv, amax), one scale per tensor or per row."""
+    groups = rows if per_row else 1
+    dst = np.empty(rows * cols, dtype=NP_DTYPE[tout])
+    sc = np.empty(groups, np.float32)
+    am = np.empty(groups, np.float32)
+    lib().orc_quantize(tin, tout, _p(np.ascontiguousarray(src)), _p(dst), rows, cols, sinv, qmax, int(per_row),
+                       _p(sc), _p(am))
+    return dst, sc, am
 
 
 # ---- GEMM ----------------------------------------------------------------------------------------

@@ -508,3 +508,40 @@ float orc_adam(const orc_adam_config *cfg, size_t count, int pdt, void *p, int g
   }
   return q ? amax_merge(amax_in, mx) : amax_in;
 }
+
+/* ---------------------------------------------------------------------------------------------
+ * Quantize with the data's own amax (binds/python/e5m2effma/tensor.py:52-74, Float8Tensor.from_float)
+ *
+ * The reference composes this from torch operations and e5ma_cast:
+ *   per tensor (:71-74): amax = x.abs().amax().clamp_min(1e-12); scale = qmax / amax;
+ *                        data = e5ma_cast(x, scale=scale) (RNE satfinite of x * scale); scale_inv = 1 / scale
+ *   per row    (:64-69): amax = x.abs().amax(dim=1).clamp_min(1e-12); scale = qmax / amax;
+ *                        data = (x * scale[:, None]).clamp(-top, top).to(fp8); scale_inv = 1 / scale
+ * with qmax = margin * top (a Python float, rounded to FP32 when it meets the FP32 tensor).  torch
+ * evaluates `scalar / tensor` as tensor.reciprocal() * scalar, so scale = fl(fl(1 / amax) * qmax), and
+ * torch's amax and clamp_min propagate NaN.  Clamping to +-top and then rounding gives the codes of
+ * the satfinite encoder for every non-NaN value; a NaN becomes the encoder's 0x7F.
+ * ------------------------------------------------------------------------------------------- */
+static inline uint32_t abs_bits_max(uint32_t m, float v) {
+  const uint32_t a = f2u(v) & 0x7FFFFFFFu; /* NaN patterns order above Inf: the maximum keeps a NaN */
+  return a > m ? a : m;
+}
+static inline float quant_scale(uint32_t abits, float qmax) {
+  const float a = abits > 0x7F800000u ? NAN : fmaxf(u2f(abits), 1e-12f);
+  const float r = 1.0f / a;
+  return r * qmax;
+}
+
+void orc_quantize(int tin, int tout, const void *src, void *dst, size_t rows, size_t cols, float sinv,
+                  float qmax, int per_row, float *scale_inv, float *amax) {
+  const size_t n = per_row ? cols : rows * cols, groups = per_row ? rows : 1;
+  for (size_t g = 0; g < groups; ++g) {
+    const size_t base = g * n;
+    uint32_t ab = 0;
+    for (size_t i = 0; i < n; ++i) ab = abs_bits_max(ab, orc_load(tin, src, base + i, sinv));
+    const float s = quant_scale(ab, qmax);
+    for (size_t i = 0; i < n; ++i) orc_store(tout, dst, base + i, orc_load(tin, src, base + i, sinv), s);
+    scale_inv[g] = 1.0f / s;
+    if (amax) amax[g] = u2f(ab);
+  }
+}

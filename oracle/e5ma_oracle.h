@@ -51,6 +51,10 @@ size_t orc_encode_selfcheck(int fmt, uint64_t start, uint64_t stop, uint64_t ste
 float orc_cast(int tin, int tout, const void *src, void *dst, size_t count, float sinv,
                float qscale, float amax_in);
 
+/* ---- quantize with the data's own amax (Float8Tensor.from_float) ---- */
+void orc_quantize(int tin, int tout, const void *src, void *dst, size_t rows, size_t cols, float sinv,
+                  float qmax, int per_row, float *scale_inv, float *amax);
+
 /* ---- GEMM ---- */
 typedef struct {
   int transa, transb, m, n, k;

@@ -16,10 +16,12 @@ FAKE = 0x10000  # a non-NULL, 16-byte aligned address that is never dereferenced
 
 
 def header_functions():
-    with open(os.path.join(ROOT, "include", "e5m2effma.h")) as f:
-        text = f.read()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(e5ma_\w+)\s*\(", text)))
+    names = set()
+    for h in ("e5m2effma.h", "e5m2effma_ext.h"):
+        with open(os.path.join(ROOT, "include", h)) as f:
+            text = re.sub(r"/\*.*?\*/", "", f.read(), flags=re.S)
+        names |= set(re.findall(r"\b(e5ma_\w+)\s*\(", text))
+    return sorted(names)
 
 
 def test_exports_every_declared_function():
@@ -103,6 +105,26 @@ def test_cast_validation():
     assert c(T(FP32), T(5)) == (1, "e5ma_cast: invalid dtype (src 3, dst 5)")
     assert c(T(FP32), T(E5M2, scaling=1)) == (1, "e5ma_cast: per-tensor scaling only")
     assert c(T(FP32), T(E5M2), 0) == (0, "")
+
+
+def test_quantize_validation():
+    """e5ma_quantize (include/e5m2effma_ext.h) rejects bad arguments before any device call"""
+    L = _lib.lib()
+    q = lambda s, d, rows=4, cols=16, qmax=448.0, sc=FAKE: (
+        L.e5ma_quantize(_lib.ref(s), _lib.ref(d), rows, cols, qmax, sc, None, None), _lib.last_error())
+    assert q(T(FP32, data=None), T(E4M3)) == (1, "e5ma_quantize: src / dst, their data or scale_inv is NULL")
+    assert q(T(FP32), T(E4M3), sc=None)[0] == 1
+    assert q(T(FP32), T(BF16)) == (1, "e5ma_quantize: src dtype 3 / dst dtype 1 (dst must be E5MA_E4M3 or E5MA_E5M2)")
+    assert q(T(FP32, scaling=1), T(E4M3)) == (1, "e5ma_quantize: src takes per-tensor scaling only")
+    assert q(T(FP32), T(E4M3, scaling=2)) == (1, "e5ma_quantize: invalid dst scaling 2")
+    assert q(T(FP32), T(E5M2), qmax=0.0) == (1, "e5ma_quantize: qmax = 0 must be positive and finite")
+    assert q(T(FP32), T(E5M2), qmax=float("inf"))[0] == 1
+    assert q(T(FP32), T(E5M2), qmax=float("nan"))[0] == 1
+    assert q(T(FP32), T(E5M2, scaling=1), rows=0) == (0, "")
+    assert q(T(FP32), T(E5M2), cols=0) == (0, "")
+    assert q(T(FP32), T(E5M2), rows=1 << 40, cols=1 << 40) == (1, "e5ma_quantize: rows x cols overflows")
+    assert q(T(FP32), T(E5M2, scaling=1), rows=1 << 24, cols=16) == (
+        1, "e5ma_quantize: per-row scaling takes at most 16777215 rows, got 16777216")
 
 
 def test_adam_validation():

@@ -221,6 +221,81 @@ def test_cast_semantics(orc):
     assert amax == 0.5
 
 
+# ---- quantize with the data's own amax (Float8Tensor.from_float) ----------------------------------
+_TOP = {4: (57344.0, torch.float8_e5m2), 0: (448.0, torch.float8_e4m3fn)}
+
+
+def _quant_inputs(rng, rows, cols):
+    x = (rng.standard_normal((rows, cols)) * np.exp(rng.uniform(-8, 8, (rows, 1)))).astype(np.float32)
+    x[1, :] = 0.0                                   # all-zero row: amax clamps to 1e-12
+    x[2, 3] = np.inf                                # Inf row: scale 0, Inf * 0 = NaN
+    x[3, 5] = np.nan                                # NaN row: NaN amax, NaN scale
+    x[4, :] = rng.standard_normal(cols).astype(np.float32) * np.float32(1e-30)  # tiny: huge scale, saturation
+    return x
+
+
+def _reference_steps(x, fp8, per_row, margin):
+    """tensor.py:60-74 (Float8Tensor.from_float) run with torch on the CPU; the per-tensor branch's
+    e5ma_cast is the oracle's cast (pinned by the encoder tests above)."""
+    import oracle
+    top, tdt = _TOP[fp8]
+    xf = torch.from_numpy(x)
+    if per_row:
+        amax = xf.abs().amax(dim=1).clamp_min(1e-12)
+        scale = margin * top / amax
+        data = (xf * scale[:, None]).clamp(-top, top).to(tdt).view(torch.uint8).numpy().reshape(-1)
+        return data, (1.0 / scale).float().numpy(), xf.abs().amax(dim=1).numpy()
+    amax = xf.abs().amax().clamp_min(1e-12).reshape(1)
+    scale = (margin * top / amax).float()
+    data, _ = oracle.cast(3, fp8, x.reshape(-1), x.size, 1.0, float(scale[0]))
+    return data, (1.0 / scale).numpy(), xf.abs().amax().reshape(1).numpy()
+
+
+def _same_f32(a, b):
+    a, b = np.asarray(a, np.float32), np.asarray(b, np.float32)
+    return np.array_equal(np.isnan(a), np.isnan(b)) and np.array_equal(a.view(np.uint32)[~np.isnan(a)],
+                                                                      b.view(np.uint32)[~np.isnan(b)])
+
+
+@pytest.mark.parametrize("fp8", [4, 0])
+@pytest.mark.parametrize("per_row", [False, True])
+@pytest.mark.parametrize("margin", [1.0, 0.9])
+def test_quantize_matches_reference_composition(orc, fp8, per_row, margin):
+    """orc_quantize against the reference's own torch steps, bit for bit: codes, scale_inv, amax.  A NaN
+    code from torch's .to(fp8) may carry the sign bit; the oracle's is 0x7F (the encoder's)."""
+    rng = np.random.default_rng(7 + fp8 + per_row)
+    rows, cols = 37, 203
+    x = _quant_inputs(rng, rows, cols)
+    top, _ = _TOP[fp8]
+    qmax = float(np.float32(margin * top))
+    got, sinv, amax = orc.quantize(3, fp8, x, rows, cols, qmax, per_row=per_row)
+    want, want_sinv, want_amax = _reference_steps(x, fp8, per_row, margin)
+    nan_code = (want & 0x7F) == 0x7F if fp8 == 0 else (want & 0x7F) > 0x7C
+    assert np.all(got[nan_code] == 0x7F)
+    assert np.array_equal(got[~nan_code], want[~nan_code])
+    assert _same_f32(sinv, want_sinv) and _same_f32(amax, want_amax)
+
+
+def test_quantize_special_cases(orc):
+    """Closed forms: a tensor whose amax is a power of two maps it exactly to qmax; the all-zero tensor
+    uses amax 1e-12; a NaN anywhere makes the per-tensor scale NaN; FP8 sources are decoded times sinv."""
+    x = np.array([[0.25, -1.0, 0.5, 0.125]], np.float32)
+    codes, sinv, amax = orc.quantize(3, 4, x, 1, 4, 57344.0)
+    assert amax[0] == 1.0 and sinv[0] == np.float32(1.0) / np.float32(57344.0)
+    assert codes.tolist() == [orc.encode(4, np.float32([14336.0]))[0], 0xFB, orc.encode(4, np.float32([28672.0]))[0],
+                              orc.encode(4, np.float32([7168.0]))[0]]
+    codes, sinv, amax = orc.quantize(3, 0, np.zeros((2, 8), np.float32), 2, 8, 448.0, per_row=True)
+    r = np.float32(1.0) / np.float32(1e-12)
+    assert np.all(codes == 0) and amax.tolist() == [0.0, 0.0]
+    assert np.all(sinv == np.float32(1.0) / (r * np.float32(448.0)))
+    codes, sinv, amax = orc.quantize(3, 4, np.array([1.0, np.nan, 2.0], np.float32), 1, 3, 57344.0)
+    assert np.isnan(amax[0]) and np.isnan(sinv[0]) and np.all(codes == 0x7F)
+    c8 = orc.encode(4, np.float32([3.0, -0.5, 0.75, 1.5]))
+    got, s1, a1 = orc.quantize(4, 0, c8, 1, 4, 448.0, sinv=0.5)
+    want, s2, a2 = orc.quantize(3, 0, orc.decode(4, c8, 0.5), 1, 4, 448.0)
+    assert np.array_equal(got, want) and s1 == s2 and a1 == a2 == 1.5
+
+
 # ---- GEMM semantics ----------------------------------------------------------------------------------
 def _rand_fp8(rng, n, fmt):
     c = rng.integers(0, 256, n).astype(np.uint8)
