@@ -13,15 +13,9 @@ using namespace dev;
 constexpr int kThreads = 256;
 constexpr int kVec = 8;
 constexpr int kNoCopy = -1;
-// launch shape: grid cap and non-temporal accesses, per state width (measured on 2^28 parameters:
-// BF16 states 5.16 TB/s with non-temporal accesses and 65536 blocks; FP32 states 4.93 TB/s with
-// ordinary accesses and 8192 blocks, where non-temporal accesses cost 15%)
-#ifndef E5MA_ADAM_GRID_BF16
-#define E5MA_ADAM_GRID_BF16 65536
-#endif
-#ifndef E5MA_ADAM_GRID_FP32
-#define E5MA_ADAM_GRID_FP32 8192
-#endif
+// launch shape: non-temporal accesses per state width (measured on 2^28 parameters: BF16 states
+// 5.16 TB/s with non-temporal accesses and 65536 blocks; FP32 states 4.93 TB/s with ordinary accesses
+// and 8192 blocks, where non-temporal accesses cost 15%); the grid caps come from the device's Tuning
 #ifndef E5MA_ADAM_NT_BF16
 #define E5MA_ADAM_NT_BF16 1
 #endif
@@ -108,13 +102,12 @@ __global__ __launch_bounds__(kThreads) void adam_kernel(AdamScalars a, size_t co
 
 template <int PT, int GT, int MT, int QT>
 hipError_t adam_v(const AdamScalars &a, size_t count, void *p, const void *g, void *m, void *v, uint8_t *q,
-                  const float *qs, float *amax, hipStream_t s) {
+                  const float *qs, float *amax, int cap, hipStream_t s) {
   const auto a16 = [](const void *x) { return ((uintptr_t)x & 15u) == 0; };
   const bool vec = a16(p) && a16(g) && a16(m) && a16(v) && ((uintptr_t)q & 7u) == 0;
   const size_t work = vec ? (count + kVec - 1) / kVec : count;
   const size_t blocks = (work + kThreads - 1) / kThreads;
-  constexpr size_t kCap = PT == E5MA_FP32 ? E5MA_ADAM_GRID_FP32 : E5MA_ADAM_GRID_BF16;
-  const int grid = (int)(blocks < kCap ? blocks : kCap);
+  const int grid = (int)(blocks < (size_t)cap ? blocks : (size_t)cap);
   if (vec) adam_kernel<PT, GT, MT, QT, true><<<grid, kThreads, 0, s>>>(a, count, p, g, m, v, q, qs, amax);
   else adam_kernel<PT, GT, MT, QT, false><<<grid, kThreads, 0, s>>>(a, count, p, g, m, v, q, qs, amax);
   return hipGetLastError();
@@ -122,33 +115,35 @@ hipError_t adam_v(const AdamScalars &a, size_t count, void *p, const void *g, vo
 
 template <int PT, int GT, int MT>
 hipError_t adam_q(int qt, const AdamScalars &a, size_t count, void *p, const void *g, void *m, void *v, uint8_t *q,
-                  const float *qs, float *amax, hipStream_t s) {
-  if (!q) return adam_v<PT, GT, MT, kNoCopy>(a, count, p, g, m, v, q, qs, amax, s);
-  if (qt == E5MA_E5M2) return adam_v<PT, GT, MT, E5MA_E5M2>(a, count, p, g, m, v, q, qs, amax, s);
-  return adam_v<PT, GT, MT, E5MA_E4M3>(a, count, p, g, m, v, q, qs, amax, s);
+                  const float *qs, float *amax, int cap, hipStream_t s) {
+  if (!q) return adam_v<PT, GT, MT, kNoCopy>(a, count, p, g, m, v, q, qs, amax, cap, s);
+  if (qt == E5MA_E5M2) return adam_v<PT, GT, MT, E5MA_E5M2>(a, count, p, g, m, v, q, qs, amax, cap, s);
+  return adam_v<PT, GT, MT, E5MA_E4M3>(a, count, p, g, m, v, q, qs, amax, cap, s);
 }
 
 template <int PT, int GT>
 hipError_t adam_m(int mt, int qt, const AdamScalars &a, size_t count, void *p, const void *g, void *m, void *v,
-                  uint8_t *q, const float *qs, float *amax, hipStream_t s) {
-  if (mt == E5MA_BF16) return adam_q<PT, GT, E5MA_BF16>(qt, a, count, p, g, m, v, q, qs, amax, s);
-  return adam_q<PT, GT, E5MA_FP32>(qt, a, count, p, g, m, v, q, qs, amax, s);
+                  uint8_t *q, const float *qs, float *amax, int cap, hipStream_t s) {
+  if (mt == E5MA_BF16) return adam_q<PT, GT, E5MA_BF16>(qt, a, count, p, g, m, v, q, qs, amax, cap, s);
+  return adam_q<PT, GT, E5MA_FP32>(qt, a, count, p, g, m, v, q, qs, amax, cap, s);
 }
 
 template <int PT>
 hipError_t adam_g(int gt, int mt, int qt, const AdamScalars &a, size_t count, void *p, const void *g, void *m,
-                  void *v, uint8_t *q, const float *qs, float *amax, hipStream_t s) {
-  if (gt == E5MA_BF16) return adam_m<PT, E5MA_BF16>(mt, qt, a, count, p, g, m, v, q, qs, amax, s);
-  if (gt == E5MA_FP16) return adam_m<PT, E5MA_FP16>(mt, qt, a, count, p, g, m, v, q, qs, amax, s);
-  return adam_m<PT, E5MA_FP32>(mt, qt, a, count, p, g, m, v, q, qs, amax, s);
+                  void *v, uint8_t *q, const float *qs, float *amax, int cap, hipStream_t s) {
+  if (gt == E5MA_BF16) return adam_m<PT, E5MA_BF16>(mt, qt, a, count, p, g, m, v, q, qs, amax, cap, s);
+  if (gt == E5MA_FP16) return adam_m<PT, E5MA_FP16>(mt, qt, a, count, p, g, m, v, q, qs, amax, cap, s);
+  return adam_m<PT, E5MA_FP32>(mt, qt, a, count, p, g, m, v, q, qs, amax, cap, s);
 }
 
 }  // namespace
 
 hipError_t launch_adam(const AdamScalars &a, size_t count, int pt, void *p, int gt, const void *g, int mt, void *m,
-                       void *v, int qt, uint8_t *q, const float *qscale, float *amax, hipStream_t s) {
-  if (pt == E5MA_BF16) return adam_g<E5MA_BF16>(gt, mt, qt, a, count, p, g, m, v, q, qscale, amax, s);
-  return adam_g<E5MA_FP32>(gt, mt, qt, a, count, p, g, m, v, q, qscale, amax, s);
+                       void *v, int qt, uint8_t *q, const float *qscale, float *amax, const Tuning &t,
+                       hipStream_t s) {
+  const int cap = pt == E5MA_BF16 ? t.adam_grid_bf16 : t.adam_grid_fp32;
+  if (pt == E5MA_BF16) return adam_g<E5MA_BF16>(gt, mt, qt, a, count, p, g, m, v, q, qscale, amax, cap > 0 ? cap : 65536, s);
+  return adam_g<E5MA_FP32>(gt, mt, qt, a, count, p, g, m, v, q, qscale, amax, cap > 0 ? cap : 8192, s);
 }
 
 }  // namespace e5ma

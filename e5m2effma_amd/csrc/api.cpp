@@ -10,6 +10,7 @@
 
 #include "e5m2effma_ext.h"
 #include "e5ma_host.hpp"
+#include "e5ma_tuned.h"
 
 namespace e5ma {
 
@@ -30,6 +31,22 @@ e5ma_status hip_status(hipError_t e, const char *what) {
   return fail(E5MA_HIP_ERROR, "%s: HIP error %d (%s): %s", what, (int)e, hipGetErrorName(e), hipGetErrorString(e));
 }
 
+// Tuned launch choices per (architecture, CU count), written by the tuner (e5m2effma_amd/tune/tune.cpp)
+struct TunedEntry {
+  const char *arch;
+  int cus;
+  Tuning t;
+};
+static const TunedEntry kTuned[] = {E5MA_TUNED_ENTRIES{nullptr, 0, {}}};
+
+static Tuning tuning_for(const char *arch, int cus) {
+  for (const TunedEntry *e = kTuned; e->arch; ++e) {
+    const size_t n = strlen(e->arch);
+    if (e->cus == cus && strncmp(arch, e->arch, n) == 0 && (arch[n] == 0 || arch[n] == ':')) return e->t;
+  }
+  return Tuning{};
+}
+
 // Per-device properties, filled once per device (reference src/e5m2effma.cu:31-51 keeps a lazy
 // per-device cache; here std::call_once makes the first use race-free).
 static constexpr int kMaxDevices = 64;
@@ -47,6 +64,7 @@ const DeviceInfo &device_info(int dev) {
     d.cus = p.multiProcessorCount;
     snprintf(d.arch, sizeof d.arch, "%s", p.gcnArchName);
     d.supported = strncmp(p.gcnArchName, "gfx950", 6) == 0;
+    d.tune = tuning_for(p.gcnArchName, d.cus);
     d.xcds = 8;
     if (d.supported) {
       hipMemPoolProps props{};
@@ -105,10 +123,12 @@ extern "C" e5ma_status e5ma_cast(const e5ma_tensor *src, const e5ma_tensor *dst,
   if (src->scaling != E5MA_SCALING_TENSOR || dst->scaling != E5MA_SCALING_TENSOR)
     return fail(E5MA_INVALID_VALUE, "e5ma_cast: per-tensor scaling only");
   if (count == 0) return E5MA_OK;
-  if (e5ma_status st = e5ma::check_device()) return st;
+  int dev = 0;
+  if (e5ma_status st = e5ma::check_device(&dev)) return st;
   const hipError_t err = e5ma::launch_cast(src->dtype, dst->dtype, src->data, dst->data, count,
                                           is_fp8(src->dtype) ? src->scale_inv : nullptr,
-                                          is_fp8(dst->dtype) ? dst->scale : nullptr, dst->amax, stream);
+                                          is_fp8(dst->dtype) ? dst->scale : nullptr, dst->amax,
+                                          e5ma::device_info(dev).tune, stream);
   return e5ma::hip_status(err, "e5ma_cast: kernel launch");
 }
 
@@ -133,10 +153,12 @@ extern "C" e5ma_status e5ma_quantize(const e5ma_tensor *src, const e5ma_tensor *
   // per row, a launch has up to 256 threads per row and HIP's grid holds fewer than 2^32 threads
   if (dst->scaling == E5MA_SCALING_OUTER && rows >= ((size_t)1 << 24))
     return fail(E5MA_INVALID_VALUE, "e5ma_quantize: per-row scaling takes at most %d rows, got %zu", (1 << 24) - 1, rows);
-  if (e5ma_status st = e5ma::check_device()) return st;
+  int dev = 0;
+  if (e5ma_status st = e5ma::check_device(&dev)) return st;
   const hipError_t err = e5ma::launch_quantize(src->dtype, dst->dtype, src->data, dst->data, rows, cols,
                                                is_fp8(src->dtype) ? src->scale_inv : nullptr, qmax,
-                                               dst->scaling == E5MA_SCALING_OUTER, scale_inv, amax_out, stream);
+                                               dst->scaling == E5MA_SCALING_OUTER, scale_inv, amax_out,
+                                               e5ma::device_info(dev).tune, stream);
   return e5ma::hip_status(err, "e5ma_quantize: kernel launch");
 }
 
@@ -164,7 +186,8 @@ extern "C" e5ma_status e5ma_adam(const e5ma_adam_config *cfg, size_t count, cons
   if (param_fp8 && param_fp8->data && param_fp8->scaling != E5MA_SCALING_TENSOR)
     return fail(E5MA_INVALID_VALUE, "e5ma_adam: param_fp8 takes per-tensor scaling only");
   if (count == 0) return E5MA_OK;
-  if (e5ma_status st = e5ma::check_device()) return st;
+  int dev = 0;
+  if (e5ma_status st = e5ma::check_device(&dev)) return st;
   // scalars formed in double and rounded to FP32 once (reference src/adamw_e5m2effma.cu:150-157)
   e5ma::AdamScalars a;
   a.lr = cfg->lr;
@@ -183,7 +206,7 @@ extern "C" e5ma_status e5ma_adam(const e5ma_adam_config *cfg, size_t count, cons
   const hipError_t err =
       e5ma::launch_adam(a, count, param->dtype, param->data, grad->dtype, grad->data, exp_avg->dtype, exp_avg->data,
                         exp_avg_sq->data, q ? (int)param_fp8->dtype : (int)E5MA_E4M3, q, q ? param_fp8->scale : nullptr,
-                        q ? param_fp8->amax : nullptr, stream);
+                        q ? param_fp8->amax : nullptr, e5ma::device_info(dev).tune, stream);
   return e5ma::hip_status(err, "e5ma_adam: kernel launch");
 }
 

@@ -11,9 +11,6 @@ namespace {
 using namespace dev;
 constexpr int kThreads = 256;
 constexpr int kVec = 16;
-#ifndef E5MA_CAST_GRID
-#define E5MA_CAST_GRID 8192
-#endif
 #ifndef E5MA_CAST_NT
 #define E5MA_CAST_NT 0
 #endif
@@ -54,11 +51,11 @@ __global__ __launch_bounds__(kThreads) void cast_kernel(const void *__restrict__
 
 template <int TI, int TO>
 hipError_t cast_to(const void *src, void *dst, size_t count, const float *sinv, const float *qs, float *amax,
-                   hipStream_t s) {
+                   int cap, hipStream_t s) {
   const bool vec = (((uintptr_t)src | (uintptr_t)dst) & 15u) == 0;
   const size_t work = vec ? (count + kVec - 1) / kVec : count;
   const size_t blocks = (work + kThreads - 1) / kThreads;
-  const int grid = (int)(blocks < E5MA_CAST_GRID ? blocks : E5MA_CAST_GRID);
+  const int grid = (int)(blocks < (size_t)cap ? blocks : (size_t)cap);
 #define E5MA_CAST_LAUNCH(V, A) \
   cast_kernel<TI, TO, V, A><<<grid, kThreads, 0, s>>>(src, dst, count, sinv, qs, amax)
   if (vec) {
@@ -72,26 +69,27 @@ hipError_t cast_to(const void *src, void *dst, size_t count, const float *sinv, 
 
 template <int TI>
 hipError_t cast_from(int tout, const void *src, void *dst, size_t count, const float *sinv, const float *qs,
-                     float *amax, hipStream_t s) {
+                     float *amax, int cap, hipStream_t s) {
   switch (tout) {
-    case E5MA_E5M2: return cast_to<TI, E5MA_E5M2>(src, dst, count, sinv, qs, amax, s);
-    case E5MA_E4M3: return cast_to<TI, E5MA_E4M3>(src, dst, count, sinv, qs, amax, s);
-    case E5MA_BF16: return cast_to<TI, E5MA_BF16>(src, dst, count, sinv, qs, amax, s);
-    case E5MA_FP16: return cast_to<TI, E5MA_FP16>(src, dst, count, sinv, qs, amax, s);
-    default: return cast_to<TI, E5MA_FP32>(src, dst, count, sinv, qs, amax, s);
+    case E5MA_E5M2: return cast_to<TI, E5MA_E5M2>(src, dst, count, sinv, qs, amax, cap, s);
+    case E5MA_E4M3: return cast_to<TI, E5MA_E4M3>(src, dst, count, sinv, qs, amax, cap, s);
+    case E5MA_BF16: return cast_to<TI, E5MA_BF16>(src, dst, count, sinv, qs, amax, cap, s);
+    case E5MA_FP16: return cast_to<TI, E5MA_FP16>(src, dst, count, sinv, qs, amax, cap, s);
+    default: return cast_to<TI, E5MA_FP32>(src, dst, count, sinv, qs, amax, cap, s);
   }
 }
 
 }  // namespace
 
 hipError_t launch_cast(int tin, int tout, const void *src, void *dst, size_t count, const float *sinv,
-                       const float *qscale, float *amax, hipStream_t s) {
+                       const float *qscale, float *amax, const Tuning &t, hipStream_t s) {
+  const int cap = t.cast_grid > 0 ? t.cast_grid : 8192;
   switch (tin) {
-    case E5MA_E5M2: return cast_from<E5MA_E5M2>(tout, src, dst, count, sinv, qscale, amax, s);
-    case E5MA_E4M3: return cast_from<E5MA_E4M3>(tout, src, dst, count, sinv, qscale, amax, s);
-    case E5MA_BF16: return cast_from<E5MA_BF16>(tout, src, dst, count, sinv, qscale, amax, s);
-    case E5MA_FP16: return cast_from<E5MA_FP16>(tout, src, dst, count, sinv, qscale, amax, s);
-    default: return cast_from<E5MA_FP32>(tout, src, dst, count, sinv, qscale, amax, s);
+    case E5MA_E5M2: return cast_from<E5MA_E5M2>(tout, src, dst, count, sinv, qscale, amax, cap, s);
+    case E5MA_E4M3: return cast_from<E5MA_E4M3>(tout, src, dst, count, sinv, qscale, amax, cap, s);
+    case E5MA_BF16: return cast_from<E5MA_BF16>(tout, src, dst, count, sinv, qscale, amax, cap, s);
+    case E5MA_FP16: return cast_from<E5MA_FP16>(tout, src, dst, count, sinv, qscale, amax, cap, s);
+    default: return cast_from<E5MA_FP32>(tout, src, dst, count, sinv, qscale, amax, cap, s);
   }
 }
 

@@ -8,9 +8,9 @@
 // applies the epilogue (alpha * sa * sb, bias, beta * C, conversion, amax).  Each split's error terms are
 // the unsplit kernel's over a part of the products, so the accumulation bound of the whole K still holds,
 // with S - 1 FP32 additions on top (S <= 256: far inside 2 k 2^-24 sum|a b|).  Splitting is used only
-// when the tiles fill at most a quarter of the CUs (2 splits of a half-filled grid measured slower than
-// none: the partials' traffic outweighs the idle half); S is then the largest divisor of the ring rounds
-// in K that keeps tiles * S <= CUs and at least two rounds per split.
+// when the tiles fill at most 1 / Tuning::splitk_div of the CUs (default 4: 2 splits of a half-filled
+// grid measured slower than none, the partials' traffic outweighing the idle half); S is then the
+// largest divisor of the ring rounds in K that keeps tiles * S <= CUs and at least two rounds per split.
 #include "e5ma_host.hpp"
 #include "gemm_common.hpp"
 
@@ -23,9 +23,9 @@ constexpr int kTile = 256;                             // the fast kernels' bloc
 constexpr long long kMaxWorkspace = 1LL << 30;         // bytes of FP32 partials, at most
 constexpr int kReduceThreads = 256;
 
-int split_count(int m, int n, int k, int round, int cus) {
+int split_count(int m, int n, int k, int round, int cus, int div) {
   const long long tiles = (long long)((m + kTile - 1) / kTile) * ((n + kTile - 1) / kTile);
-  if (tiles * 4 > cus) return 1;
+  if (div <= 0 || tiles * div > cus) return 1;
   const int rounds = k / round;
   const long long ldw = (m + 3) & ~3LL;
   int best = 1;
@@ -68,7 +68,7 @@ typedef hipError_t (*FastLaunch)(int, int, bool, bool, const uint8_t *, long lon
 hipError_t launch_fast(FastLaunch launch, int round, int at, int bt, bool akc, bool bkc, const uint8_t *A, long long lda,
                        const uint8_t *B, long long ldb, int m, int n, int k, const Epilogue &e, const DeviceInfo &di,
                        hipStream_t s) {
-  const int splits = split_count(m, n, k, round, di.cus > 0 ? di.cus : 256);
+  const int splits = split_count(m, n, k, round, di.cus > 0 ? di.cus : 256, di.tune.splitk_div);
   if (splits > 1) {
     const long long ldw = (m + 3) & ~3LL;
     void *ws = nullptr;

@@ -23,7 +23,6 @@ namespace {
 using namespace dev;
 constexpr int kThreads = 256;
 constexpr int kVec = 16;
-constexpr int kGrid = 8192;
 
 __device__ __forceinline__ uint32_t abs_bits_max(uint32_t m, float v) {
   const uint32_t a = f2u(v) & 0x7FFFFFFFu;
@@ -200,7 +199,7 @@ __global__ __launch_bounds__(kThreads) void q_rows_blk_kernel(const void *__rest
 
 template <int TI, int TO>
 hipError_t quantize_to(const void *src, void *dst, size_t rows, size_t cols, const float *sinv, float qmax,
-                       bool per_row, float *scale_inv, float *amax, hipStream_t s) {
+                       bool per_row, float *scale_inv, float *amax, int cap, hipStream_t s) {
   if (per_row) {
     const bool vec = cols % kVec == 0 && (((uintptr_t)src | (uintptr_t)dst) & 15u) == 0;
     const size_t blocks = (rows + kThreads / 64 - 1) / (kThreads / 64);
@@ -217,7 +216,7 @@ hipError_t quantize_to(const void *src, void *dst, size_t rows, size_t cols, con
   const bool vec = (((uintptr_t)src | (uintptr_t)dst) & 15u) == 0;
   const size_t work = vec ? (count + kVec - 1) / kVec : count;
   const size_t blocks = (work + kThreads - 1) / kThreads;
-  const int grid = (int)(blocks < kGrid ? blocks : kGrid);
+  const int grid = (int)(blocks < (size_t)cap ? blocks : (size_t)cap);
   uint32_t *word = (uint32_t *)scale_inv;
   q_clear_kernel<<<1, 1, 0, s>>>(word);
   if (vec) {
@@ -233,21 +232,22 @@ hipError_t quantize_to(const void *src, void *dst, size_t rows, size_t cols, con
 
 template <int TI>
 hipError_t quantize_from(int tout, const void *src, void *dst, size_t rows, size_t cols, const float *sinv,
-                         float qmax, bool per_row, float *scale_inv, float *amax, hipStream_t s) {
-  if (tout == E5MA_E5M2) return quantize_to<TI, E5MA_E5M2>(src, dst, rows, cols, sinv, qmax, per_row, scale_inv, amax, s);
-  return quantize_to<TI, E5MA_E4M3>(src, dst, rows, cols, sinv, qmax, per_row, scale_inv, amax, s);
+                         float qmax, bool per_row, float *scale_inv, float *amax, int cap, hipStream_t s) {
+  if (tout == E5MA_E5M2) return quantize_to<TI, E5MA_E5M2>(src, dst, rows, cols, sinv, qmax, per_row, scale_inv, amax, cap, s);
+  return quantize_to<TI, E5MA_E4M3>(src, dst, rows, cols, sinv, qmax, per_row, scale_inv, amax, cap, s);
 }
 
 }  // namespace
 
 hipError_t launch_quantize(int tin, int tout, const void *src, void *dst, size_t rows, size_t cols, const float *sinv,
-                           float qmax, bool per_row, float *scale_inv, float *amax, hipStream_t s) {
+                           float qmax, bool per_row, float *scale_inv, float *amax, const Tuning &t, hipStream_t s) {
+  const int cap = t.cast_grid > 0 ? t.cast_grid : 8192;
   switch (tin) {
-    case E5MA_E5M2: return quantize_from<E5MA_E5M2>(tout, src, dst, rows, cols, sinv, qmax, per_row, scale_inv, amax, s);
-    case E5MA_E4M3: return quantize_from<E5MA_E4M3>(tout, src, dst, rows, cols, sinv, qmax, per_row, scale_inv, amax, s);
-    case E5MA_BF16: return quantize_from<E5MA_BF16>(tout, src, dst, rows, cols, sinv, qmax, per_row, scale_inv, amax, s);
-    case E5MA_FP16: return quantize_from<E5MA_FP16>(tout, src, dst, rows, cols, sinv, qmax, per_row, scale_inv, amax, s);
-    default: return quantize_from<E5MA_FP32>(tout, src, dst, rows, cols, sinv, qmax, per_row, scale_inv, amax, s);
+    case E5MA_E5M2: return quantize_from<E5MA_E5M2>(tout, src, dst, rows, cols, sinv, qmax, per_row, scale_inv, amax, cap, s);
+    case E5MA_E4M3: return quantize_from<E5MA_E4M3>(tout, src, dst, rows, cols, sinv, qmax, per_row, scale_inv, amax, cap, s);
+    case E5MA_BF16: return quantize_from<E5MA_BF16>(tout, src, dst, rows, cols, sinv, qmax, per_row, scale_inv, amax, cap, s);
+    case E5MA_FP16: return quantize_from<E5MA_FP16>(tout, src, dst, rows, cols, sinv, qmax, per_row, scale_inv, amax, cap, s);
+    default: return quantize_from<E5MA_FP32>(tout, src, dst, rows, cols, sinv, qmax, per_row, scale_inv, amax, cap, s);
   }
 }
 

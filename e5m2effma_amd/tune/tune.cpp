@@ -1,0 +1,223 @@
+// tune.cpp -- times the launch-choice candidates of struct Tuning (e5m2effma_amd/csrc/e5ma_host.hpp) on
+// device 0 and records the winners for its (architecture, CU count) in e5ma_tuned.h, keeping the other
+// devices' entries (the reference's tune/tune.cu:18-166 does the same for its GEMM / GEMV tables).
+// Like the reference's tuner it calls the kernel launchers directly (exported by libe5m2effma.so)
+// with a candidate Tuning, not through the C ABI.  A candidate replaces the default only if it is at
+// least 2% faster; each time is the best of 7 runs of a batch of calls (hipEvent timing).
+//
+//   e5ma_tune [header] [--dry-run]       tune, print the entry, and (unless --dry-run) rewrite header
+//   e5ma_tune --emit header arch cus splitk_div cast_grid adam_grid_bf16 adam_grid_fp32 [name]
+//                                        rewrite header with that entry, no device use (tests)
+//
+// Workloads (the BASELINE shapes of each choice):
+//   cast_grid       FP32 -> E5M2 cast of 8192^2 elements, two sources rotated past the Infinity Cache
+//   adam_grid_*     AdamW over 2^28 parameters, BF16 resp. FP32 state, with an E5M2 copy
+//   splitk_div      E5M2 x E5M2 -> BF16 TN GEMMs with at most 64 tiles: 512^2, 1024^2, 2048^2, 4096 x 1024
+//                   and 8192 x 64, all with k = 8192 (summed)
+#include <hip/hip_runtime.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <fstream>
+#include <string>
+#include <vector>
+
+#include "e5ma_host.hpp"
+
+using namespace e5ma;
+
+static void check(hipError_t e, const char *what) {
+  if (e != hipSuccess) {
+    fprintf(stderr, "%s: %s\n", what, hipGetErrorString(e));
+    exit(1);
+  }
+}
+
+template <class F> static float best_ms(F f, int batch, int reps = 7) {
+  hipEvent_t a, b;
+  check(hipEventCreate(&a), "hipEventCreate");
+  check(hipEventCreate(&b), "hipEventCreate");
+  for (int i = 0; i < batch; ++i) check(f(i), "warm-up launch");
+  check(hipDeviceSynchronize(), "hipDeviceSynchronize");
+  float best = 1e30f;
+  for (int r = 0; r < reps; ++r) {
+    check(hipEventRecord(a, nullptr), "hipEventRecord");
+    for (int i = 0; i < batch; ++i) check(f(i), "launch");
+    check(hipEventRecord(b, nullptr), "hipEventRecord");
+    check(hipEventSynchronize(b), "hipEventSynchronize");
+    float ms = 0;
+    check(hipEventElapsedTime(&ms, a, b), "hipEventElapsedTime");
+    if (ms / batch < best) best = ms / batch;
+  }
+  check(hipEventDestroy(a), "hipEventDestroy");
+  check(hipEventDestroy(b), "hipEventDestroy");
+  return best;
+}
+
+// the candidate with the best time, unless it beats the default's time by less than 2%
+static int pick(const char *what, const std::vector<int> &cands, const std::vector<float> &ms, int def) {
+  const float kMargin = 0.98f;
+  size_t bi = 0, di = 0;
+  for (size_t i = 0; i < cands.size(); ++i) {
+    printf("  %-16s %8d  %9.4f ms\n", what, cands[i], ms[i]);
+    if (ms[i] < ms[bi]) bi = i;
+    if (cands[i] == def) di = i;
+  }
+  const int best = ms[bi] <= kMargin * ms[di] ? cands[bi] : def;
+  printf("  -> %s = %d\n", what, best);
+  return best;
+}
+
+static void *dalloc(size_t bytes, int fill) {
+  void *p = nullptr;
+  check(hipMalloc(&p, bytes), "hipMalloc");
+  check(hipMemset(p, fill, bytes), "hipMemset");
+  return p;
+}
+
+static Tuning tune_device(const DeviceInfo &di) {
+  Tuning t = di.tune, def;
+  // ---- cast ----
+  {
+    const size_t n = (size_t)8192 * 8192;
+    void *src[2] = {dalloc(n * 4, 0x3C), dalloc(n * 4, 0x3D)};
+    void *dst = dalloc(n, 0);
+    float *qs = (float *)dalloc(4, 0);
+    const std::vector<int> cands = {2048, 4096, 8192, 16384, 32768};
+    std::vector<float> ms;
+    for (int c : cands) {
+      Tuning x = def;
+      x.cast_grid = c;
+      ms.push_back(best_ms([&](int i) { return launch_cast(E5MA_FP32, E5MA_E5M2, src[i & 1], dst, n, nullptr, nullptr, nullptr, x, nullptr); }, 10));
+    }
+    printf("cast FP32 -> E5M2, 8192^2\n");
+    t.cast_grid = pick("cast_grid", cands, ms, def.cast_grid);
+    check(hipFree(src[0]), "hipFree");
+    check(hipFree(src[1]), "hipFree");
+    check(hipFree(dst), "hipFree");
+    check(hipFree(qs), "hipFree");
+  }
+  // ---- AdamW, 2^28 parameters ----
+  for (int pt : {E5MA_BF16, E5MA_FP32}) {
+    const size_t n = (size_t)1 << 28, es = pt == E5MA_BF16 ? 2 : 4;
+    void *p = dalloc(n * es, 0x3C), *g = dalloc(n * es, 0x3A), *m = dalloc(n * es, 0x38), *v = dalloc(n * es, 0x30);
+    uint8_t *q = (uint8_t *)dalloc(n, 0);
+    AdamScalars a{};
+    a.lr = 1e-4f; a.beta1 = 0.9f; a.beta2 = 0.999f; a.omb1 = 0.1f; a.omb2 = 0.001f; a.rbc1 = 1.f; a.rbc2 = 1.f;
+    a.eps = 1e-8f; a.lr_wd = 1e-6f; a.wd = 0.01f; a.gscale = 1.f; a.adamw = 1;
+    const std::vector<int> cands = pt == E5MA_BF16 ? std::vector<int>{16384, 32768, 65536, 131072}
+                                                   : std::vector<int>{4096, 8192, 16384, 32768};
+    std::vector<float> ms;
+    for (int c : cands) {
+      Tuning x = def;
+      (pt == E5MA_BF16 ? x.adam_grid_bf16 : x.adam_grid_fp32) = c;
+      ms.push_back(best_ms([&](int) { return launch_adam(a, n, pt, p, pt, g, pt, m, v, E5MA_E5M2, q, nullptr, nullptr, x, nullptr); }, 3));
+    }
+    printf("AdamW 2^28 parameters, %s state\n", pt == E5MA_BF16 ? "BF16" : "FP32");
+    if (pt == E5MA_BF16) t.adam_grid_bf16 = pick("adam_grid_bf16", cands, ms, def.adam_grid_bf16);
+    else t.adam_grid_fp32 = pick("adam_grid_fp32", cands, ms, def.adam_grid_fp32);
+    for (void *b : {p, g, m, v, (void *)q}) check(hipFree(b), "hipFree");
+  }
+  // ---- split-K threshold ----
+  {
+    struct Shape { int m, n, k; };
+    const Shape shapes[] = {{512, 512, 8192}, {1024, 1024, 8192}, {2048, 2048, 8192}, {4096, 1024, 8192}, {8192, 64, 8192}};
+    const size_t big = (size_t)8192 * 8192;
+    uint8_t *A = (uint8_t *)dalloc(big, 0x33), *B = (uint8_t *)dalloc(big, 0x35);
+    void *D = dalloc(big * 2, 0);
+    const std::vector<int> cands = {0, 2, 4, 8};
+    std::vector<float> ms;
+    for (int c : cands) {
+      DeviceInfo x = di;
+      x.tune = def;
+      x.tune.splitk_div = c;
+      float sum = 0;
+      for (const Shape &s : shapes) {
+        dev::Epilogue e{};
+        e.alpha = 1.f;
+        e.d = D;
+        e.ldd = s.m;
+        e.d_dtype = E5MA_BF16;
+        e.c_dtype = E5MA_FP32;
+        e.bias_dtype = E5MA_FP32;
+        sum += best_ms([&](int) { return launch_gemm(E5MA_E5M2, E5MA_E5M2, true, true, A, s.k, B, s.k, s.m, s.n, s.k, e, x, nullptr); }, 5);
+      }
+      ms.push_back(sum);
+    }
+    printf("GEMM TN E5M2 x E5M2 -> BF16, k = 8192, m x n in {512^2, 1024^2, 2048^2, 4096 x 1024, 8192 x 64} (summed)\n");
+    t.splitk_div = pick("splitk_div", cands, ms, def.splitk_div);
+    for (void *b : {(void *)A, (void *)B, D}) check(hipFree(b), "hipFree");
+  }
+  return t;
+}
+
+// rewrite the header: every entry line of other devices, then this device's
+static int emit(const char *path, const char *arch, int cus, const Tuning &t, const char *name) {
+  std::vector<std::string> keep;
+  {
+    std::ifstream in(path);
+    std::string line;
+    char ea[64];
+    int ec = 0;
+    while (std::getline(in, line)) {
+      const size_t pos = line.find("/* entry arch=");
+      if (pos == std::string::npos) continue;
+      if (sscanf(line.c_str() + pos, "/* entry arch=%63s cus=%d", ea, &ec) == 2 && !(strcmp(ea, arch) == 0 && ec == cus))
+        keep.push_back(line);
+    }
+  }
+  char buf[512];
+  snprintf(buf, sizeof buf, "  {\"%s\", %d, {%d, %d, %d, %d}}, /* entry arch=%s cus=%d tuned on %s */ \\", arch, cus,
+           t.splitk_div, t.cast_grid, t.adam_grid_bf16, t.adam_grid_fp32, arch, cus, name);
+  keep.push_back(buf);
+  std::ofstream out(path);
+  if (!out) {
+    fprintf(stderr, "cannot write %s\n", path);
+    return 1;
+  }
+  out << "// e5ma_tuned.h -- written by the tuner (e5m2effma_amd/tune/tune.cpp; make -C e5m2effma_amd/csrc tune-run):\n"
+         "// per-device launch choices of struct Tuning (e5ma_host.hpp), one entry per (architecture, CU count):\n"
+         "// {arch, cus, {splitk_div, cast_grid, adam_grid_bf16, adam_grid_fp32}}.  Re-running the tuner on a\n"
+         "// device adds or replaces that device's entry and keeps the others.\n"
+         "#pragma once\n#define E5MA_TUNED_ENTRIES \\\n";
+  for (const std::string &l : keep) out << l << "\n";
+  out << "\n";
+  printf("wrote %s: %s\n", path, buf);
+  return 0;
+}
+
+int main(int argc, char **argv) {
+  if (argc >= 9 && strcmp(argv[1], "--emit") == 0) {
+    Tuning t;
+    t.splitk_div = atoi(argv[5]);
+    t.cast_grid = atoi(argv[6]);
+    t.adam_grid_bf16 = atoi(argv[7]);
+    t.adam_grid_fp32 = atoi(argv[8]);
+    return emit(argv[2], argv[3], atoi(argv[4]), t, argc > 9 ? argv[9] : "unnamed device");
+  }
+  const char *path = "e5m2effma_amd/csrc/e5ma_tuned.h";
+  bool dry = false;
+  for (int i = 1; i < argc; ++i) {
+    if (strcmp(argv[i], "--dry-run") == 0) dry = true;
+    else path = argv[i];
+  }
+  check(hipSetDevice(0), "hipSetDevice");
+  if (e5ma_status st = check_device()) {
+    fprintf(stderr, "device 0 is not supported (status %d)\n", (int)st);
+    return 1;
+  }
+  const DeviceInfo &di = device_info(0);
+  hipDeviceProp_t p;
+  check(hipGetDeviceProperties(&p, 0), "hipGetDeviceProperties");
+  char arch[64];
+  snprintf(arch, sizeof arch, "%s", p.gcnArchName);
+  if (char *c = strchr(arch, ':')) *c = 0;
+  char name[256];
+  snprintf(name, sizeof name, "%s", p.name[0] ? p.name : "an unnamed device");  // empty without amdgpu.ids
+  printf("tuning on %s (%s, %d CUs)\n", name, arch, di.cus);
+  const Tuning t = tune_device(di);
+  printf("entry: {\"%s\", %d, {%d, %d, %d, %d}}\n", arch, di.cus, t.splitk_div, t.cast_grid, t.adam_grid_bf16,
+         t.adam_grid_fp32);
+  return dry ? 0 : emit(path, arch, di.cus, t, name);
+}
