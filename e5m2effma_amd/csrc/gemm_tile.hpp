@@ -297,6 +297,87 @@ __device__ __forceinline__ float direct_epilogue(const Epilogue &e, v16f (&acc)[
   return mx;
 }
 
+// The direct epilogue of a full tile with a bias and / or beta * C (C of dtype CT, -1 when beta = 0, with
+// 4-element aligned columns): the direct epilogue's layout and column order, with C read in that same
+// layout, 16 bytes (FP32) per lane and (x, g).  Units u = 4 y + x (4 loads each, g = 0..3) stream
+// through a ring of kSlots units, refilled as each unit is consumed: 24 loads per lane in flight
+// (96 VGPRs), where staging through LDS, 8 columns per thread per step, kept a third of that in flight.
+// The bias of the tile's 256 rows goes to LDS once (FP32).  Same operation order as general_half:
+// v = acc * ((alpha * sa[i]) * sb[j]); v + bias[i]; fma(beta, C, v).  C may alias D: each element is
+// loaded before the same thread stores it.  All threads of the block must call it (two barriers).
+template <int DT, int CT>
+__device__ __forceinline__ float direct_general(const Epilogue &e, v16f (&acc)[4][4], int i0, int j0, int wm, int wn,
+                                                int lane, int tid) {
+  constexpr int kSlots = 6;
+  float mx = 0.f;
+  const EpiState st = epi_begin(e);
+  const int ib0 = i0 + 128 * wm + 4 * (lane >> 5);
+  const float sa1 = e.alpha * scale_or_one(e.sa), sb1 = scale_or_one(e.sb);
+  float *bias_lds = stage_at(0);
+  __syncthreads();  // the ring is no longer read
+  bias_lds[tid] = e.bias ? load_any(e.bias_dtype, e.bias, (size_t)(i0 + tid), 1.f) : 0.f;
+  __syncthreads();
+  float cv[kSlots][4][4];
+  const auto load_unit = [&](int u, float (&c)[4][4]) {
+    const int y = u >> 2, x = u & 3;
+    const size_t at = (size_t)(j0 + 128 * wn + 32 * y + (lane & 31)) * e.ldc + ib0 + 32 * x;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) load4_t<CT>(e.c, at + 8 * g, st.csinv, c[g]);
+  };
+  if constexpr (CT >= 0) {
+#pragma unroll
+    for (int u = 0; u < kSlots; ++u) load_unit(u, cv[u]);
+  }
+#pragma unroll
+  for (int u = 0; u < 16; ++u) {
+    const int y = u >> 2, x = u & 3;
+    const int j = j0 + 128 * wn + 32 * y + (lane & 31);
+    const float sbj = e.sb_vec ? e.sb[j] : sb1;
+    uint8_t *colp = (uint8_t *)e.d + ((size_t)j * e.ldd + ib0 + 32 * x) * elem_bytes(DT);
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      __builtin_amdgcn_sched_barrier(0);
+      const int il = 128 * wm + 32 * x + 8 * g + 4 * (lane >> 5);
+      const float4 b4 = *(const float4 *)(bias_lds + il);
+      const float rb[4] = {b4.x, b4.y, b4.z, b4.w};
+      float as[4];
+      if (e.sa_vec) {
+        const float4 v = *(const float4 *)(e.sa + i0 + il);
+        as[0] = e.alpha * v.x; as[1] = e.alpha * v.y; as[2] = e.alpha * v.z; as[3] = e.alpha * v.w;
+      } else {
+        as[0] = as[1] = as[2] = as[3] = sa1;
+      }
+      float v[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float sc = (e.sa_vec || e.sb_vec) ? as[q] * sbj : st.s;
+        v[q] = acc_read(acc[x][y][4 * g + q]) * sc;
+        if (e.bias) v[q] = v[q] + rb[q];
+        if constexpr (CT >= 0) v[q] = __builtin_fmaf(e.beta, cv[u % kSlots][g][q], v[q]);
+        mx = amax_fold(mx, v[q]);
+      }
+      uint8_t *dp = colp + 8 * g * elem_bytes(DT);
+      if constexpr (DT == E5MA_FP32) {
+        *(float4 *)dp = make_float4(v[0], v[1], v[2], v[3]);
+      } else if constexpr (is_fp8(DT)) {
+        *(uint32_t *)dp = encode_t<DT>(v[0], st.qscale) | encode_t<DT>(v[1], st.qscale) << 8 |
+                          encode_t<DT>(v[2], st.qscale) << 16 | encode_t<DT>(v[3], st.qscale) << 24;
+      } else if constexpr (DT == E5MA_BF16) {
+        *(uint2 *)dp = bf16_quad(v);
+      } else {
+        *(uint2 *)dp = make_uint2(encode_t<DT>(v[0], 1.f) | encode_t<DT>(v[1], 1.f) << 16,
+                                  encode_t<DT>(v[2], 1.f) | encode_t<DT>(v[3], 1.f) << 16);
+      }
+    }
+    // unit u's slot is free: refill it with unit u + kSlots
+    if constexpr (CT >= 0) {
+      __builtin_amdgcn_sched_barrier(0);
+      if (u + kSlots < 16) load_unit(u + kSlots, cv[u % kSlots]);
+    }
+  }
+  return mx;
+}
+
 // The epilogue of a block tile (acc: this wave's accumulators; i0, j0: the tile's origin).  Returns the
 // thread's max |value| for amax.
 template <int DT>
@@ -312,6 +393,12 @@ __device__ __forceinline__ float tile_epilogue(const TileArgs &t, const Epilogue
     // no bias, beta = 0, a full tile, D aligned for 4-element stores
     mx = e.amax ? direct_epilogue<DT, true>(e, acc, i0, j0, wm, wn, lane)
                 : direct_epilogue<DT, false>(e, acc, i0, j0, wm, wn, lane);
+  } else if (vec && i0 + kBM <= t.m && j0 + kBN <= t.n &&
+             (e.beta == 0.f ||
+              (e.c_dtype == E5MA_FP32 && (uintptr_t)e.c % 16 == 0 && e.ldc % 4 == 0))) {
+    // a full tile with a bias and / or beta * FP32 C (TE's wgrad into main_grad), D and C aligned
+    mx = e.beta != 0.f ? direct_general<DT, E5MA_FP32>(e, acc, i0, j0, wm, wn, lane, tid)
+                       : direct_general<DT, -1>(e, acc, i0, j0, wm, wn, lane, tid);
   } else {
     // general epilogue (bias, beta * C, tails): half a tile at a time -- the 128 columns of the waves
     // with wn == h, 256 x 128 FP32 = the whole ring, column group c (16 columns) in ring buffer c --

@@ -57,13 +57,13 @@ def operand(rng, dt, size, dist="codes", sigma=1.0):
 class GemmCase:
     """One e5ma_gemm call: seeded operands, the GPU run through the C ABI, the oracle check.
 
-    transa / transb: 1 = T.  sa / sb: None, a float (per tensor) or an array (OUTER scaling).  ldd: leading
-    dimension of D (default m + 3).
+    transa / transb: 1 = T.  sa / sb: None, a float (per tensor) or an array (OUTER scaling).  ldd / ldc:
+    leading dimensions of D / C (default m + 3 / m + 5).
     beta != 0 with cdt None accumulates into D (C = NULL); otherwise C of dtype cdt is read."""
 
     def __init__(self, rng, transa, transb, m, n, k, adt, bdt, *, ddt=oracle.FP32, alpha=1.0, sa=None, sb=None,
                  beta=0.0, cdt=None, csinv=1.0, biasdt=None, qscale=None, amax=False, pad=16, dist="codes",
-                 sigma=1.0, A=None, B=None, D0=None, ldd=None):
+                 sigma=1.0, A=None, B=None, D0=None, ldd=None, ldc=None):
         self.transa, self.transb, self.m, self.n, self.k = transa, transb, m, n, k
         self.adt, self.bdt, self.ddt, self.alpha, self.beta = adt, bdt, ddt, alpha, beta
         self.lda = (k if transa else m) + pad
@@ -80,7 +80,7 @@ class GemmCase:
         self.C = None
         self.ldc = 0
         if beta != 0.0 and cdt is not None:
-            self.ldc = m + 5
+            self.ldc = ldc if ldc is not None else m + 5
             self.C = operand(rng, cdt, self.ldc * n) if cdt in FP8 else \
                 oracle.encode(cdt, rng.uniform(-4, 4, self.ldc * n).astype(np.float32)) if cdt != oracle.FP32 else \
                 rng.uniform(-4, 4, self.ldc * n).astype(np.float32)

@@ -441,3 +441,37 @@ def test_direct_epilogue_h(dev, bdt):
     assert s == 0
     bad, first = case.check(D, samples=4096, rng=rng)
     assert bad == 0, first
+
+
+# ---- the direct epilogue with a bias and / or beta * FP32 C (full tiles, D and C columns 16-byte aligned)
+# on unsplit grids: TE's wgrad into main_grad (C = NULL, beta = 1), a separate C, linear layers with a bias
+@pytest.mark.parametrize("mode,ddt", [("bias", B16), ("bias", E5), ("acc", F32), ("acc_bias", F32), ("c_bias", F32),
+                                      ("c", B16)])
+@pytest.mark.parametrize("ta,tb", LAYOUTS)
+def test_direct_general_epilogue_f8(dev, ta, tb, mode, ddt):
+    rng = np.random.default_rng(10200 + ta * 2 + tb + 10 * ddt + len(mode))
+    m, n, k = 2304, 2048, 8192
+    sa = rng.uniform(0.5, 2.0, m).astype(np.float32) * (1 / 64)
+    sb = rng.uniform(0.5, 2.0, n).astype(np.float32) * (1 / 64)
+    beta = 0.0 if mode == "bias" else 1.0 if mode.startswith("acc") else -0.5
+    case = gu.GemmCase(rng, ta, tb, m, n, k, E5, E4, ddt=ddt, alpha=0.5, sa=sa, sb=sb, beta=beta,
+                       cdt=F32 if mode.startswith("c") else None, biasdt=(B16 if ddt != F32 else F32) if "bias" in mode
+                       else None, dist="normal", sigma=8.0, pad=0, ldd=m + 4, ldc=m + 8, amax=True,
+                       qscale=0.25 if ddt in (E5, E4) else None)
+    s, D, amax = case.run(dev)
+    assert s == 0
+    bad, first = case.check(D, amax, samples=4096, rng=rng)
+    assert bad == 0, first
+
+
+@pytest.mark.parametrize("mode", ["acc_bias", "c"])
+def test_direct_general_epilogue_h(dev, mode):
+    rng = np.random.default_rng(10300 + len(mode))
+    m, n, k = 2304, 2304, 1024
+    case = gu.GemmCase(rng, 1, 0, m, n, k, E4, B16, ddt=F32, sa=0.5, beta=1.0 if mode == "acc_bias" else 0.25,
+                       cdt=None if mode == "acc_bias" else F32, biasdt=F32 if mode == "acc_bias" else None,
+                       dist="normal", sigma=2.0, pad=0, ldd=m + 4, ldc=m + 4)
+    s, D, _ = case.run(dev)
+    assert s == 0
+    bad, first = case.check(D, samples=4096, rng=rng)
+    assert bad == 0, first
