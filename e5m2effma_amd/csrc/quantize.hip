@@ -241,7 +241,7 @@ hipError_t quantize_from(int tout, const void *src, void *dst, size_t rows, size
 
 hipError_t launch_quantize(int tin, int tout, const void *src, void *dst, size_t rows, size_t cols, const float *sinv,
                            float qmax, bool per_row, float *scale_inv, float *amax, const Tuning &t, hipStream_t s) {
-  const int cap = t.cast_grid > 0 ? t.cast_grid : 8192;
+  const int cap = t.quant_grid > 0 ? t.quant_grid : 8192;
   switch (tin) {
     case E5MA_E5M2: return quantize_from<E5MA_E5M2>(tout, src, dst, rows, cols, sinv, qmax, per_row, scale_inv, amax, cap, s);
     case E5MA_E4M3: return quantize_from<E5MA_E4M3>(tout, src, dst, rows, cols, sinv, qmax, per_row, scale_inv, amax, cap, s);

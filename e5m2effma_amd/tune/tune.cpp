@@ -6,11 +6,12 @@
 // least 2% faster; each time is the best of 7 runs of a batch of calls (hipEvent timing).
 //
 //   e5ma_tune [header] [--dry-run]       tune, print the entry, and (unless --dry-run) rewrite header
-//   e5ma_tune --emit header arch cus splitk_div cast_grid adam_grid_bf16 adam_grid_fp32 [name]
+//   e5ma_tune --emit header arch cus splitk_div cast_grid adam_grid_bf16 adam_grid_fp32 quant_grid [name]
 //                                        rewrite header with that entry, no device use (tests)
 //
 // Workloads (the BASELINE shapes of each choice):
 //   cast_grid       FP32 -> E5M2 cast of 8192^2 elements, two sources rotated past the Infinity Cache
+//   quant_grid      per-tensor FP32 -> E5M2 quantize of 8192^2 elements (amax pass + scaled cast), same sources
 //   adam_grid_*     AdamW over 2^28 parameters, BF16 resp. FP32 state, with an E5M2 copy
 //   splitk_div      E5M2 x E5M2 -> BF16 TN GEMMs with at most 64 tiles: 512^2, 1024^2, 2048^2, 4096 x 1024
 //                   and 8192 x 64, all with k = 8192 (summed)
@@ -93,6 +94,15 @@ static Tuning tune_device(const DeviceInfo &di) {
     }
     printf("cast FP32 -> E5M2, 8192^2\n");
     t.cast_grid = pick("cast_grid", cands, ms, def.cast_grid);
+    const std::vector<int> qc = {512, 1024, 2048, 4096, 8192, 16384};
+    std::vector<float> qms;
+    for (int c : qc) {
+      Tuning x = def;
+      x.quant_grid = c;
+      qms.push_back(best_ms([&](int i) { return launch_quantize(E5MA_FP32, E5MA_E5M2, src[i & 1], dst, 1, n, nullptr, 57344.f, false, qs, nullptr, x, nullptr); }, 10));
+    }
+    printf("quantize FP32 -> E5M2 per tensor, 8192^2\n");
+    t.quant_grid = pick("quant_grid", qc, qms, def.quant_grid);
     check(hipFree(src[0]), "hipFree");
     check(hipFree(src[1]), "hipFree");
     check(hipFree(dst), "hipFree");
@@ -168,8 +178,8 @@ static int emit(const char *path, const char *arch, int cus, const Tuning &t, co
     }
   }
   char buf[512];
-  snprintf(buf, sizeof buf, "  {\"%s\", %d, {%d, %d, %d, %d}}, /* entry arch=%s cus=%d tuned on %s */ \\", arch, cus,
-           t.splitk_div, t.cast_grid, t.adam_grid_bf16, t.adam_grid_fp32, arch, cus, name);
+  snprintf(buf, sizeof buf, "  {\"%s\", %d, {%d, %d, %d, %d, %d}}, /* entry arch=%s cus=%d tuned on %s */ \\", arch, cus,
+           t.splitk_div, t.cast_grid, t.adam_grid_bf16, t.adam_grid_fp32, t.quant_grid, arch, cus, name);
   keep.push_back(buf);
   std::ofstream out(path);
   if (!out) {
@@ -178,8 +188,8 @@ static int emit(const char *path, const char *arch, int cus, const Tuning &t, co
   }
   out << "// e5ma_tuned.h -- written by the tuner (e5m2effma_amd/tune/tune.cpp; make -C e5m2effma_amd/csrc tune-run):\n"
          "// per-device launch choices of struct Tuning (e5ma_host.hpp), one entry per (architecture, CU count):\n"
-         "// {arch, cus, {splitk_div, cast_grid, adam_grid_bf16, adam_grid_fp32}}.  Re-running the tuner on a\n"
-         "// device adds or replaces that device's entry and keeps the others.\n"
+         "// {arch, cus, {splitk_div, cast_grid, adam_grid_bf16, adam_grid_fp32, quant_grid}}.  Re-running the\n"
+         "// tuner on a device adds or replaces that device's entry and keeps the others.\n"
          "#pragma once\n#define E5MA_TUNED_ENTRIES \\\n";
   for (const std::string &l : keep) out << l << "\n";
   out << "\n";
@@ -188,13 +198,14 @@ static int emit(const char *path, const char *arch, int cus, const Tuning &t, co
 }
 
 int main(int argc, char **argv) {
-  if (argc >= 9 && strcmp(argv[1], "--emit") == 0) {
+  if (argc >= 10 && strcmp(argv[1], "--emit") == 0) {
     Tuning t;
     t.splitk_div = atoi(argv[5]);
     t.cast_grid = atoi(argv[6]);
     t.adam_grid_bf16 = atoi(argv[7]);
     t.adam_grid_fp32 = atoi(argv[8]);
-    return emit(argv[2], argv[3], atoi(argv[4]), t, argc > 9 ? argv[9] : "unnamed device");
+    t.quant_grid = atoi(argv[9]);
+    return emit(argv[2], argv[3], atoi(argv[4]), t, argc > 10 ? argv[10] : "unnamed device");
   }
   const char *path = "e5m2effma_amd/csrc/e5ma_tuned.h";
   bool dry = false;
@@ -217,7 +228,7 @@ int main(int argc, char **argv) {
   snprintf(name, sizeof name, "%s", p.name[0] ? p.name : "an unnamed device");  // empty without amdgpu.ids
   printf("tuning on %s (%s, %d CUs)\n", name, arch, di.cus);
   const Tuning t = tune_device(di);
-  printf("entry: {\"%s\", %d, {%d, %d, %d, %d}}\n", arch, di.cus, t.splitk_div, t.cast_grid, t.adam_grid_bf16,
-         t.adam_grid_fp32);
+  printf("entry: {\"%s\", %d, {%d, %d, %d, %d, %d}}\n", arch, di.cus, t.splitk_div, t.cast_grid, t.adam_grid_bf16,
+         t.adam_grid_fp32, t.quant_grid);
   return dry ? 0 : emit(path, arch, di.cus, t, name);
 }

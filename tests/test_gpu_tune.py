@@ -18,8 +18,9 @@ def test_tuner_dry_run():
     r = subprocess.run([TUNER, "--dry-run"], capture_output=True, text=True, timeout=300, cwd=ROOT)
     print(r.stdout)
     assert r.returncode == 0, r.stderr
-    m = re.search(r'entry: \{"(gfx950)", (\d+), \{(-?\d+), (\d+), (\d+), (\d+)\}\}', r.stdout)
+    m = re.search(r'entry: \{"(gfx950)", (\d+), \{(-?\d+), (\d+), (\d+), (\d+), (\d+)\}\}', r.stdout)
     assert m, r.stdout
-    split, cast, abf, af32 = map(int, m.groups()[2:])
+    split, cast, abf, af32, quant = map(int, m.groups()[2:])
     assert split in (0, 2, 4, 8) and cast in (2048, 4096, 8192, 16384, 32768)
     assert abf in (16384, 32768, 65536, 131072) and af32 in (4096, 8192, 16384, 32768)
+    assert quant in (512, 1024, 2048, 4096, 8192, 16384)
