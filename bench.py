@@ -263,6 +263,28 @@ def main():
                               "roofline": roof("hbm", gbs, HBM_PEAK_GBS, "GB/s", f"gemv_8192_n{n}")})
         del Ws, sas
 
+        # the same kernel's streaming rate: 8x the rows (512 MiB of weights, two buffers rotated past the
+        # Infinity Cache), where the per-call fixed cost (launch gap, ramp-up, tail) weighs 8x less
+        M8 = 8 * M
+        Wb = [torch.randint(0, 0x7B, (M8 * Kd,), dtype=torch.uint8, device=dev, generator=g) for _ in range(2)]
+        sa8 = torch.full((M8,), 1.0 / 64, dtype=torch.float32, device=dev)
+        x = torch.randn(Kd, device=dev, generator=g).to(torch.bfloat16)
+        y = torch.empty(M8, dtype=torch.bfloat16, device=dev)
+        descs = [_lib.tensor(w.data_ptr(), E5M2, sa8.data_ptr(), None, None, 1) for w in Wb]
+        Bt, Dt = _lib.tensor(x.data_ptr(), BF16), _lib.tensor(y.data_ptr(), BF16)
+
+        def f(i=0):
+            check(L.e5ma_gemm(1, 0, M8, 1, Kd, 1.0, ctypes.byref(descs[i % 2]), Kd, ctypes.byref(Bt), Kd, 0.0, None, 0,
+                              ctypes.byref(Dt), M8, None, sp), "gemv")
+        ms = timed(f, max(K, 30), W)
+        nbytes = M8 * Kd + M8 * 4 + Kd * 2 + M8 * 2
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        secondary.append({"workload": "gemv 65536x8192 E5M2 x BF16 n=1 -> BF16 (streaming rate of the n=1 kernel)",
+                          "id": "gemv_65536x8192_n1", "value": round(gbs, 1), "unit": "GB/s",
+                          "ms_per_call": round(ms, 5), "bytes_per_call": nbytes,
+                          "roofline": roof("hbm", gbs, HBM_PEAK_GBS, "GB/s", "gemv_65536x8192_n1")})
+        del Wb
+
     # ---- AdamW 256M parameters ----------------------------------------------------------------------
     if "adam" in only:
         n = 256 * 1024 * 1024
