@@ -23,7 +23,7 @@ struct Tuning {
   int cast_grid = 8192;        // block cap of the grid-stride cast and quantize kernels
   int adam_grid_bf16 = 65536;  // block cap of the Adam kernel with BF16 parameters
   int adam_grid_fp32 = 8192;   // ... with FP32 parameters
-  int quant_grid = 8192;       // block cap of the per-tensor quantize passes (amax, then the scaled cast)
+  int quant_grid = 8192;       // block cap of the per-tensor quantize's amax pass (its cast pass: cast_grid)
 };
 
 struct DeviceInfo {

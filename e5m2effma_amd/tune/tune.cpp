@@ -11,7 +11,8 @@
 //
 // Workloads (the BASELINE shapes of each choice):
 //   cast_grid       FP32 -> E5M2 cast of 8192^2 elements, two sources rotated past the Infinity Cache
-//   quant_grid      per-tensor FP32 -> E5M2 quantize of 8192^2 elements (amax pass + scaled cast), same sources
+//   quant_grid      the amax pass of a per-tensor FP32 -> E5M2 quantize of 8192^2 elements (timed as the whole
+//                   call, its cast pass at the cast_grid just chosen), same sources
 //   adam_grid_*     AdamW over 2^28 parameters, BF16 resp. FP32 state, with an E5M2 copy
 //   splitk_div      E5M2 x E5M2 -> BF16 TN GEMMs with at most 64 tiles: 512^2, 1024^2, 2048^2, 4096 x 1024
 //                   and 8192 x 64, all with k = 8192 (summed)
@@ -98,6 +99,7 @@ static Tuning tune_device(const DeviceInfo &di) {
     std::vector<float> qms;
     for (int c : qc) {
       Tuning x = def;
+      x.cast_grid = t.cast_grid;
       x.quant_grid = c;
       qms.push_back(best_ms([&](int i) { return launch_quantize(E5MA_FP32, E5MA_E5M2, src[i & 1], dst, 1, n, nullptr, 57344.f, false, qs, nullptr, x, nullptr); }, 10));
     }
