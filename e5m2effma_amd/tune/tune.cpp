@@ -3,7 +3,9 @@
 // devices' entries (the reference's tune/tune.cu:18-166 does the same for its GEMM / GEMV tables).
 // Like the reference's tuner it calls the kernel launchers directly (exported by libe5m2effma.so)
 // with a candidate Tuning, not through the C ABI.  A candidate replaces the default only if it is at
-// least 2% faster; each time is the best of 7 runs of a batch of calls (hipEvent timing).
+// least 2% faster; each time is the best of 7 runs of a batch of calls (hipEvent timing).  The cast and
+// quantize candidates' outputs (codes, scale_inv, amax) are compared bit for bit with the first
+// candidate's on varied inputs; one that differs is reported and never picked.
 //
 //   e5ma_tune [header] [--dry-run]       tune, print the entry, and (unless --dry-run) rewrite header
 //   e5ma_tune --emit header arch cus splitk_div cast_grid adam_grid_bf16 adam_grid_fp32 quant_grid [name]
@@ -17,6 +19,7 @@
 //   splitk_div      E5M2 x E5M2 -> BF16 TN GEMMs with at most 64 tiles: 512^2, 1024^2, 2048^2, 4096 x 1024
 //                   and 8192 x 64, all with k = 8192 (summed)
 #include <hip/hip_runtime.h>
+#include <math.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
@@ -57,15 +60,19 @@ template <class F> static float best_ms(F f, int batch, int reps = 7) {
   return best;
 }
 
-// the candidate with the best time, unless it beats the default's time by less than 2%
-static int pick(const char *what, const std::vector<int> &cands, const std::vector<float> &ms, int def) {
+// the candidate with the best time, unless it beats the default's time by less than 2%; a candidate
+// whose output differed from the first candidate's (ok[i] false) is never picked
+static int pick(const char *what, const std::vector<int> &cands, const std::vector<float> &ms, int def,
+                const std::vector<bool> &ok = {}) {
   const float kMargin = 0.98f;
   size_t bi = 0, di = 0;
   for (size_t i = 0; i < cands.size(); ++i) {
-    printf("  %-16s %8d  %9.4f ms\n", what, cands[i], ms[i]);
-    if (ms[i] < ms[bi]) bi = i;
+    const bool good = ok.empty() || ok[i];
+    printf("  %-16s %8d  %9.4f ms%s\n", what, cands[i], ms[i], good ? "" : "  (output differs: rejected)");
     if (cands[i] == def) di = i;
   }
+  for (size_t i = 0; i < cands.size(); ++i)
+    if ((ok.empty() || ok[i]) && (ms[i] < ms[bi] || !(ok.empty() || ok[bi]))) bi = i;
   const int best = ms[bi] <= kMargin * ms[di] ? cands[bi] : def;
   printf("  -> %s = %d\n", what, best);
   return best;
@@ -78,33 +85,77 @@ static void *dalloc(size_t bytes, int fill) {
   return p;
 }
 
+// the bytes of a device buffer
+static std::vector<uint8_t> fetch(const void *p, size_t bytes) {
+  std::vector<uint8_t> h(bytes);
+  check(hipMemcpy(h.data(), p, bytes, hipMemcpyDeviceToHost), "hipMemcpy");
+  return h;
+}
+
 static Tuning tune_device(const DeviceInfo &di) {
   Tuning t = di.tune, def;
-  // ---- cast ----
+  int checked = 0, differing = 0;
+  // ---- cast and quantize (their outputs are compared with the first candidate's, bit for bit) ----
   {
     const size_t n = (size_t)8192 * 8192;
     void *src[2] = {dalloc(n * 4, 0x3C), dalloc(n * 4, 0x3D)};
+    {  // varied values in src[0]: a sum of uniforms (roughly normal) over 12 decades, every 997th negated
+      std::vector<float> h(n);
+      uint32_t r = 0xE5A00Fu;
+      for (size_t i = 0; i < n; ++i) {
+        float v = 0.f;
+        for (int q = 0; q < 4; ++q) { r ^= r << 13; r ^= r >> 17; r ^= r << 5; v += (float)(r >> 8) * 0x1p-24f - 0.5f; }
+        h[i] = v * ldexpf(1.f, (int)(i % 40) - 20) * (i % 997 ? 1.f : -1.f);
+      }
+      check(hipMemcpy(src[0], h.data(), n * 4, hipMemcpyHostToDevice), "hipMemcpy");
+    }
     void *dst = dalloc(n, 0);
     float *qs = (float *)dalloc(4, 0);
     const std::vector<int> cands = {2048, 4096, 8192, 16384, 32768};
     std::vector<float> ms;
+    std::vector<bool> ok;
+    std::vector<uint8_t> ref;
+    float *amax = (float *)dalloc(4, 0);
+    const float qscale = 1024.f;
+    float *qsc = (float *)dalloc(4, 0);
+    check(hipMemcpy(qsc, &qscale, 4, hipMemcpyHostToDevice), "hipMemcpy");
     for (int c : cands) {
       Tuning x = def;
       x.cast_grid = c;
       ms.push_back(best_ms([&](int i) { return launch_cast(E5MA_FP32, E5MA_E5M2, src[i & 1], dst, n, nullptr, nullptr, nullptr, x, nullptr); }, 10));
+      check(hipMemset(amax, 0, 4), "hipMemset");
+      check(launch_cast(E5MA_FP32, E5MA_E5M2, src[0], dst, n, nullptr, qsc, amax, x, nullptr), "launch");
+      std::vector<uint8_t> out = fetch(dst, n), am = fetch(amax, 4);
+      out.insert(out.end(), am.begin(), am.end());
+      if (ref.empty()) ref = out;
+      ok.push_back(out == ref);
+      ++checked;
+      differing += out != ref;
     }
     printf("cast FP32 -> E5M2, 8192^2\n");
-    t.cast_grid = pick("cast_grid", cands, ms, def.cast_grid);
+    t.cast_grid = pick("cast_grid", cands, ms, def.cast_grid, ok);
     const std::vector<int> qc = {512, 1024, 2048, 4096, 8192, 16384};
     std::vector<float> qms;
+    ok.clear();
+    ref.clear();
     for (int c : qc) {
       Tuning x = def;
       x.cast_grid = t.cast_grid;
       x.quant_grid = c;
       qms.push_back(best_ms([&](int i) { return launch_quantize(E5MA_FP32, E5MA_E5M2, src[i & 1], dst, 1, n, nullptr, 57344.f, false, qs, nullptr, x, nullptr); }, 10));
+      check(launch_quantize(E5MA_FP32, E5MA_E5M2, src[0], dst, 1, n, nullptr, 57344.f, false, qs, amax, x, nullptr), "launch");
+      std::vector<uint8_t> out = fetch(dst, n), sc = fetch(qs, 4), am = fetch(amax, 4);
+      out.insert(out.end(), sc.begin(), sc.end());
+      out.insert(out.end(), am.begin(), am.end());
+      if (ref.empty()) ref = out;
+      ok.push_back(out == ref);
+      ++checked;
+      differing += out != ref;
     }
     printf("quantize FP32 -> E5M2 per tensor, 8192^2\n");
-    t.quant_grid = pick("quant_grid", qc, qms, def.quant_grid);
+    t.quant_grid = pick("quant_grid", qc, qms, def.quant_grid, ok);
+    check(hipFree(amax), "hipFree");
+    check(hipFree(qsc), "hipFree");
     check(hipFree(src[0]), "hipFree");
     check(hipFree(src[1]), "hipFree");
     check(hipFree(dst), "hipFree");
@@ -161,6 +212,8 @@ static Tuning tune_device(const DeviceInfo &di) {
     t.splitk_div = pick("splitk_div", cands, ms, def.splitk_div);
     for (void *b : {(void *)A, (void *)B, D}) check(hipFree(b), "hipFree");
   }
+  printf("outputs of %d cast / quantize candidates compared with their first candidate's: %d differ\n", checked,
+         differing);
   return t;
 }
 

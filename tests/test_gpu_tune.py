@@ -1,7 +1,8 @@
 """The tuner on the GPU (e5m2effma_amd/tune/e5ma_tune --dry-run): it times every candidate of every launch
 choice through the library's launchers and reports an entry whose values are among the candidates.
-Launch choices never change results: the cast and Adam are grid-stride kernels, and split-K is held to
-the same bound by the GEMM tests with and without it."""
+Launch choices never change results: the tuner compares the cast and quantize candidates' outputs bit for
+bit (none may differ), Adam is grid-stride like them, and split-K is held to the same bound by the GEMM
+tests with and without it."""
 import os
 import re
 import subprocess
@@ -24,3 +25,6 @@ def test_tuner_dry_run():
     assert split in (0, 2, 4, 8) and cast in (2048, 4096, 8192, 16384, 32768)
     assert abf in (16384, 32768, 65536, 131072) and af32 in (4096, 8192, 16384, 32768)
     assert quant in (512, 1024, 2048, 4096, 8192, 16384)
+    # every cast / quantize candidate produced the same codes, scale_inv and amax
+    assert re.search(r"outputs of 11 cast / quantize candidates compared with their first candidate's: 0 differ",
+                     r.stdout), r.stdout
