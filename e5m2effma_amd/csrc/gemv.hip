@@ -438,9 +438,104 @@ __global__ __launch_bounds__(kXThreads) void gemv_xlds_kernel(const uint8_t *A, 
   if (e.amax) amax_commit_block(e.amax, mx, red);
 }
 
+// ---- matrix-core kernel for 5 <= n <= 8 with BF16 or FP8 x ----------------------------------------
+// A block owns 16 rows and reduces them over all of k on v_mfma_f32_16x16x32_bf16: operand A is the 16
+// rows of weights widened exactly to BF16, operand B is x widened the same way (BF16 x as is), with
+// columns n .. 15 of the 16-column operand zero.  Lane l (row / column r = l & 15, k-group g = l >> 4)
+// reads U 16-byte chunks of its row, c = cw + 4 u + g: load u of a wave reads 64 contiguous bytes of
+// each of its 16 rows (16 lines per instruction), and a batch 64 U contiguous bytes per row; MFMA (u, h) takes k 16 c + 8 h .. + 7 for A from the lane's
+// weights and for B from column r of x at the same k.  Any assignment of k to the 32 slots of one MFMA is
+// a valid reduction order as long as A and B use the same one, and they do: a lane's k depend on g only.
+// Products are exact and accumulate in FP32, so the result meets the same bound as the dot kernels.
+// The W waves of a block take every W-th batch; their 16 x 16 partial results are summed in wave order
+// through LDS (deterministic), then 16 n threads run the epilogue.  x comes from L2 per wave with no
+// LDS copy, so a CU holds several blocks, and x bytes are 2 n / 16 of the weight bytes per block.
+// Replaces the dot kernels' per-weight x traffic (16 B of x from LDS per weight dword at n = 8).
+// Measured on 8192 x 8192 E5M2 x BF16 (us, dot kernel -> this one, 4 chunks, 4 waves): n = 3 15.5 -> 19.5,
+// n = 4 17.6 -> 19.6, n = 5 22.3 -> 19.9, n = 6 23.2 -> 20.0, n = 7 24.1 -> 21.0, n = 8 24.7 -> 21.7; 8 chunks
+// or 8 waves per block were no faster (8 chunks: 128 VGPRs), so n <= 4 stays on the dot kernels.
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+#ifndef E5MA_GEMV_MFMA_U
+#define E5MA_GEMV_MFMA_U 4  // 16-byte chunks per lane and batch
+#endif
+#ifndef E5MA_GEMV_MFMA_WAVES
+#define E5MA_GEMV_MFMA_WAVES 4
+#endif
+constexpr int kMWaves = E5MA_GEMV_MFMA_WAVES, kMThreads = 64 * kMWaves;
+
+template <int AT, int BT, int NB, int U>
+__global__ __launch_bounds__(kMThreads) void gemv_mfma_kernel(const uint8_t *A, long long lda, const uint8_t *B,
+                                                             long long ldb, int m, int k, Epilogue e) {
+  __shared__ float part[kMWaves][16][17];
+  __shared__ float red[kMWaves];
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r = lane & 15, g = lane >> 4;
+  const int i0 = blockIdx.x * 16;
+  const int nch = k >> 4;
+  const EpiState st = epi_begin(e);
+  GemvOut<NB> out;
+  out.fetch(e, st, i0, m, 16, tid);
+  const uint8_t *arow = A + (long long)min(i0 + r, m - 1) * lda;  // rows past m: never stored
+  const bool xlane = r < NB;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int cw = wave * 4 * U; cw < nch; cw += kMWaves * 4 * U) {
+    const int cl = cw + g;
+    u32x4 wa[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      wa[u] = __builtin_nontemporal_load((const u32x4 *)(arow + 16 * min(cl + 4 * u, nch - 1)));
+    XChunk<BT> xc[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (xlane) {
+        xc[u].load(B, ldb, r, min(cl + 4 * u, nch - 1));
+      } else {
+#pragma unroll
+        for (int d = 0; d < XChunk<BT>::kDw; ++d) xc[u].w[d] = 0u;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const bool valid = cl + 4 * u < nch;
+      bf16x2 xp[8], wp[8];
+      xc[u].pairs(xp, valid && xlane);
+#pragma unroll
+      for (int d = 0; d < 4; ++d) fp8x4_to_bf16<AT>(valid ? wa[u][d] : 0u, wp[2 * d], wp[2 * d + 1]);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const u32x4 aw = {__builtin_bit_cast(uint32_t, wp[4 * h]), __builtin_bit_cast(uint32_t, wp[4 * h + 1]),
+                          __builtin_bit_cast(uint32_t, wp[4 * h + 2]), __builtin_bit_cast(uint32_t, wp[4 * h + 3])};
+        const u32x4 bw = {__builtin_bit_cast(uint32_t, xp[4 * h]), __builtin_bit_cast(uint32_t, xp[4 * h + 1]),
+                          __builtin_bit_cast(uint32_t, xp[4 * h + 2]), __builtin_bit_cast(uint32_t, xp[4 * h + 3])};
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, aw), __builtin_bit_cast(bf16x8, bw),
+                                                      acc, 0, 0, 0);
+      }
+    }
+  }
+  // lane l holds outputs (row 4 g + q, column r) of its wave's partial result
+#pragma unroll
+  for (int q = 0; q < 4; ++q) part[wave][4 * g + q][r] = acc[q];
+  __syncthreads();
+  float mx = 0.f;
+  if (out.r >= 0 && i0 + out.r < m) {
+    float sum = part[0][out.r][out.j];
+#pragma unroll
+    for (int w = 1; w < kMWaves; ++w) sum += part[w][out.r][out.j];
+    const float v = out.finish(e, sum);
+    store_any(e.d_dtype, e.d, (size_t)out.j * e.ldd + i0 + out.r, v, st.qscale);
+    mx = amax_fold(0.f, v);
+  }
+  if (e.amax) amax_commit_block(e.amax, mx, red);
+}
+
 template <int AT, int BT, int NB>
 hipError_t gemv_n(const uint8_t *A, long long lda, const uint8_t *B, long long ldb, int m, int k, const Epilogue &e,
                   hipStream_t s) {
+  if constexpr (BT != E5MA_FP32 && NB >= 5) {
+    gemv_mfma_kernel<AT, BT, NB, E5MA_GEMV_MFMA_U><<<(m + 15) / 16, kMThreads, 0, s>>>(A, lda, B, ldb, m, k, e);
+    return hipGetLastError();
+  }
   if constexpr (BT != E5MA_FP32) {
     const long long xbytes = (long long)k * NB * elem_bytes(BT);
     if (xbytes <= kXLds) {
