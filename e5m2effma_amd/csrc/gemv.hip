@@ -6,7 +6,9 @@
 // reads 1 KiB contiguous per row and pass), decodes them with the packed FP8 -> FP32 converts, and
 // FMAs them against the matching x values of every column.  The 64 partial sums of each output are
 // combined by a butterfly over the wave; lane r*n + j then runs the epilogue of output (row r, j).
-// No matrix cores: every weight byte is read once from HBM and used for n FMAs.
+// Every weight byte is read once from HBM.  Up to n = 4 (and for FP32 x) the products run on the
+// VALU; at n = 5 .. 8 with a BF16 or FP8 x, gemv_mfma_kernel reduces 16 rows per block on the BF16
+// matrix cores.
 #include "e5ma_host.hpp"
 
 namespace e5ma {
