@@ -466,6 +466,60 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 #endif
 constexpr int kMWaves = E5MA_GEMV_MFMA_WAVES, kMThreads = 64 * kMWaves;
 
+// One batch of gemv_mfma_kernel: U chunks per lane (c = cl + 4 u) loaded, widened and multiplied.  FULL
+// batches (every chunk inside the row: the wave-uniform cw + 4 U <= nch) take unclamped addresses and no
+// masks; the last, partial batch clamps its addresses and zeroes out-of-range chunks as whole 32-bit words
+// (weights and x both, so that no x value past the row end meets a weight).
+template <int AT, int BT, int U, bool FULL>
+__device__ __forceinline__ void gemv_mfma_batch(const uint8_t *arow, const uint8_t *B, long long ldb, int r, bool xlane,
+                                                int cl, int nch, f32x4 &acc) {
+  u32x4 wa[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u)
+    wa[u] = __builtin_nontemporal_load((const u32x4 *)(arow + 16 * (FULL ? cl + 4 * u : min(cl + 4 * u, nch - 1))));
+  XChunk<BT> xc[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    if (xlane) {
+      xc[u].load(B, ldb, r, FULL ? cl + 4 * u : min(cl + 4 * u, nch - 1));
+    } else {
+#pragma unroll
+      for (int d = 0; d < XChunk<BT>::kDw; ++d) xc[u].w[d] = 0u;
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const uint32_t keep = FULL || cl + 4 * u < nch ? ~0u : 0u;
+    uint32_t aw[8], bw[8];
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      bf16x2 lo, hi;
+      fp8x4_to_bf16<AT>(wa[u][d] & keep, lo, hi);
+      aw[2 * d] = __builtin_bit_cast(uint32_t, lo);
+      aw[2 * d + 1] = __builtin_bit_cast(uint32_t, hi);
+    }
+    if constexpr (is_fp8(BT)) {
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        bf16x2 lo, hi;
+        fp8x4_to_bf16<BT>(xc[u].w[d] & keep, lo, hi);
+        bw[2 * d] = __builtin_bit_cast(uint32_t, lo);
+        bw[2 * d + 1] = __builtin_bit_cast(uint32_t, hi);
+      }
+    } else {
+#pragma unroll
+      for (int d = 0; d < 8; ++d) bw[d] = xc[u].w[d] & keep;
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const u32x4 av = {aw[4 * h], aw[4 * h + 1], aw[4 * h + 2], aw[4 * h + 3]};
+      const u32x4 bv = {bw[4 * h], bw[4 * h + 1], bw[4 * h + 2], bw[4 * h + 3]};
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, av), __builtin_bit_cast(bf16x8, bv), acc,
+                                                    0, 0, 0);
+    }
+  }
+}
+
 template <int AT, int BT, int NB, int U>
 __global__ __launch_bounds__(kMThreads) void gemv_mfma_kernel(const uint8_t *A, long long lda, const uint8_t *B,
                                                              long long ldb, int m, int k, Epilogue e) {
@@ -482,38 +536,8 @@ __global__ __launch_bounds__(kMThreads) void gemv_mfma_kernel(const uint8_t *A, 
   const bool xlane = r < NB;
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   for (int cw = wave * 4 * U; cw < nch; cw += kMWaves * 4 * U) {
-    const int cl = cw + g;
-    u32x4 wa[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u)
-      wa[u] = __builtin_nontemporal_load((const u32x4 *)(arow + 16 * min(cl + 4 * u, nch - 1)));
-    XChunk<BT> xc[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      if (xlane) {
-        xc[u].load(B, ldb, r, min(cl + 4 * u, nch - 1));
-      } else {
-#pragma unroll
-        for (int d = 0; d < XChunk<BT>::kDw; ++d) xc[u].w[d] = 0u;
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const bool valid = cl + 4 * u < nch;
-      bf16x2 xp[8], wp[8];
-      xc[u].pairs(xp, valid && xlane);
-#pragma unroll
-      for (int d = 0; d < 4; ++d) fp8x4_to_bf16<AT>(valid ? wa[u][d] : 0u, wp[2 * d], wp[2 * d + 1]);
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const u32x4 aw = {__builtin_bit_cast(uint32_t, wp[4 * h]), __builtin_bit_cast(uint32_t, wp[4 * h + 1]),
-                          __builtin_bit_cast(uint32_t, wp[4 * h + 2]), __builtin_bit_cast(uint32_t, wp[4 * h + 3])};
-        const u32x4 bw = {__builtin_bit_cast(uint32_t, xp[4 * h]), __builtin_bit_cast(uint32_t, xp[4 * h + 1]),
-                          __builtin_bit_cast(uint32_t, xp[4 * h + 2]), __builtin_bit_cast(uint32_t, xp[4 * h + 3])};
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, aw), __builtin_bit_cast(bf16x8, bw),
-                                                      acc, 0, 0, 0);
-      }
-    }
+    if (cw + 4 * U <= nch) gemv_mfma_batch<AT, BT, U, true>(arow, B, ldb, r, xlane, cw + g, nch, acc);
+    else gemv_mfma_batch<AT, BT, U, false>(arow, B, ldb, r, xlane, cw + g, nch, acc);
   }
   // lane l holds outputs (row 4 g + q, column r) of its wave's partial result
 #pragma unroll
