@@ -11,8 +11,13 @@ namespace {
 using namespace dev;
 constexpr int kThreads = 256;
 constexpr int kVec = 16;
-#ifndef E5MA_CAST_NT
-#define E5MA_CAST_NT 0
+// Non-temporal accesses per side (measured on 8192^2 FP32 -> E5M2: ordinary loads and stores 61.5 us,
+// non-temporal stores only 59.3 us, non-temporal loads only 83.0 us, both non-temporal 20 % slower)
+#ifndef E5MA_CAST_NT_IN
+#define E5MA_CAST_NT_IN 0
+#endif
+#ifndef E5MA_CAST_NT_OUT
+#define E5MA_CAST_NT_OUT 1
 #endif
 
 template <int TI, int TO, bool VEC, bool AMAX>
@@ -27,9 +32,9 @@ __global__ __launch_bounds__(kThreads) void cast_kernel(const void *__restrict__
   if constexpr (VEC) {
     const size_t nvec = count / kVec;
     for (size_t c = tid; c < nvec; c += stride) {
-      Pack<TI, kVec, E5MA_CAST_NT> in;
+      Pack<TI, kVec, E5MA_CAST_NT_IN> in;
       in.load(src, c * kVec);
-      Pack<TO, kVec, E5MA_CAST_NT> out;
+      Pack<TO, kVec, E5MA_CAST_NT_OUT> out;
       out.clear();
 #pragma unroll
       for (int e = 0; e < kVec; ++e) {
