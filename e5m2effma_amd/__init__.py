@@ -203,9 +203,13 @@ def matmul(a: torch.Tensor, b: torch.Tensor, *, out_dtype: Optional[torch.dtype]
                         _scalar_ptr(amax_out, dev, "amax_out"))
         BIAS = _lib.tensor(bias.data_ptr(), _CODE[bias.dtype]) if bias is not None else None
         ldd = N if M <= 1 else out.stride(0)
-        s = _lib.lib().e5ma_gemm(transa, transb, N, M, K, float(alpha), ctypes.byref(A), ldb_, ctypes.byref(B), lda_,
-                                 float(beta), None, 0, ctypes.byref(D), ldd, _lib.ref(BIAS), _stream())
-    _check_status(s, "e5ma_gemm")
+        # split-K workspace for small grids from torch's allocator, freed in stream order after the call
+        ws_bytes = _lib.workspace_size(transa, transb, N, M, K, _CODE[b.dtype], ldb_, _CODE[a.dtype], lda_)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
+        s = _lib.lib().e5ma_gemm_ex(transa, transb, N, M, K, float(alpha), ctypes.byref(A), ldb_, ctypes.byref(B),
+                                    lda_, float(beta), None, 0, ctypes.byref(D), ldd, _lib.ref(BIAS),
+                                    None if ws is None else ws.data_ptr(), ws_bytes, _stream())
+    _check_status(s, "e5ma_gemm_ex")
     return out
 
 

@@ -15,7 +15,8 @@ OK, INVALID_VALUE, NOT_SUPPORTED, HIP_ERROR = 0, 1, 2, 3
 SCALING_TENSOR, SCALING_OUTER = 0, 1
 
 # every symbol include/e5m2effma.h and include/e5m2effma_ext.h declare
-EXPORTS = ("e5ma_gemm", "e5ma_cast", "e5ma_adam", "e5ma_status_string", "e5ma_last_error", "e5ma_quantize")
+EXPORTS = ("e5ma_gemm", "e5ma_cast", "e5ma_adam", "e5ma_status_string", "e5ma_last_error", "e5ma_quantize",
+           "e5ma_gemm_ex", "e5ma_gemm_workspace_size")
 
 
 class Tensor(ctypes.Structure):
@@ -46,6 +47,10 @@ def lib():
         TP = ctypes.POINTER(Tensor)
         L.e5ma_gemm.restype = I
         L.e5ma_gemm.argtypes = [I, I, I, I, I, F, TP, I, TP, I, F, TP, I, TP, I, TP, P]
+        L.e5ma_gemm_ex.restype = I
+        L.e5ma_gemm_ex.argtypes = [I, I, I, I, I, F, TP, I, TP, I, F, TP, I, TP, I, TP, P, S, P]
+        L.e5ma_gemm_workspace_size.restype = I
+        L.e5ma_gemm_workspace_size.argtypes = [I, I, I, I, I, I, I, I, I, ctypes.POINTER(S)]
         L.e5ma_cast.restype = I
         L.e5ma_cast.argtypes = [TP, TP, S, P]
         L.e5ma_quantize.restype = I
@@ -75,3 +80,12 @@ def tensor(data=None, dtype=FP32, scale_inv=None, scale=None, amax=None, scaling
 
 def ref(t):
     return None if t is None else ctypes.byref(t)
+
+
+def workspace_size(transa, transb, m, n, k, adt, lda, bdt, ldb):
+    """Bytes of split-K workspace e5ma_gemm_ex uses for this GEMM on the current device (0: none)."""
+    out = ctypes.c_size_t(0)
+    s = lib().e5ma_gemm_workspace_size(transa, transb, m, n, k, adt, lda, bdt, ldb, ctypes.byref(out))
+    if s != OK:
+        raise RuntimeError(f"e5ma_gemm_workspace_size: {status_string(s)}: {last_error()}")
+    return out.value

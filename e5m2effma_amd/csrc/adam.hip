@@ -26,18 +26,20 @@ constexpr int kNoCopy = -1;
 // One element in the documented order (include/e5m2effma.h:88-94; reference
 // src/adamw_e5m2effma.cu:17-25).  Division and square root are correctly rounded (the library is
 // built with -fhip-fp32-correctly-rounded-divide-sqrt and without fast-math); nothing is contracted.
-__device__ __forceinline__ void adam_elem(const AdamScalars &a, float g, float &p, float &m, float &v) {
-  g = g * a.gscale;
-  if (!a.adamw) g = __builtin_fmaf(a.wd, p, g);
-  m = __builtin_fmaf(a.beta1, m, a.omb1 * g);
-  v = __builtin_fmaf(a.beta2, v, a.omb2 * (g * g));
-  const float u = (m * a.rbc1) / (__builtin_sqrtf(v * a.rbc2) + a.eps);
-  if (a.adamw) p = __builtin_fmaf(-a.lr_wd, p, p);
+// The mode flag, not the coefficient's value, selects the weight-decay term: fma(0, p, g) is not g when
+// p is Inf or NaN.
+__device__ __forceinline__ void adam_elem(const AdamCoefficients &a, float g, float &p, float &m, float &v) {
+  g = g * a.grad_mul;
+  if (!a.decoupled) g = __builtin_fmaf(a.l2, p, g);
+  m = __builtin_fmaf(a.b1, m, a.c1 * g);
+  v = __builtin_fmaf(a.b2, v, a.c2 * (g * g));
+  const float u = (m * a.corr1) / (__builtin_sqrtf(v * a.corr2) + a.eps);
+  if (a.decoupled) p = __builtin_fmaf(-a.decay, p, p);
   p = __builtin_fmaf(-a.lr, u, p);
 }
 
 template <int PT, int GT, int MT, int QT, bool VEC>
-__global__ __launch_bounds__(kThreads) void adam_kernel(AdamScalars a, size_t count, void *__restrict__ p_,
+__global__ __launch_bounds__(kThreads) void adam_kernel(AdamCoefficients a, size_t count, void *__restrict__ p_,
                                                         const void *__restrict__ g_, void *__restrict__ m_,
                                                         void *__restrict__ v_, uint8_t *__restrict__ q_,
                                                         const float *qscale_p, float *amax) {
@@ -101,7 +103,7 @@ __global__ __launch_bounds__(kThreads) void adam_kernel(AdamScalars a, size_t co
 }
 
 template <int PT, int GT, int MT, int QT>
-hipError_t adam_v(const AdamScalars &a, size_t count, void *p, const void *g, void *m, void *v, uint8_t *q,
+hipError_t adam_v(const AdamCoefficients &a, size_t count, void *p, const void *g, void *m, void *v, uint8_t *q,
                   const float *qs, float *amax, int cap, hipStream_t s) {
   const auto a16 = [](const void *x) { return ((uintptr_t)x & 15u) == 0; };
   const bool vec = a16(p) && a16(g) && a16(m) && a16(v) && ((uintptr_t)q & 7u) == 0;
@@ -114,7 +116,7 @@ hipError_t adam_v(const AdamScalars &a, size_t count, void *p, const void *g, vo
 }
 
 template <int PT, int GT, int MT>
-hipError_t adam_q(int qt, const AdamScalars &a, size_t count, void *p, const void *g, void *m, void *v, uint8_t *q,
+hipError_t adam_q(int qt, const AdamCoefficients &a, size_t count, void *p, const void *g, void *m, void *v, uint8_t *q,
                   const float *qs, float *amax, int cap, hipStream_t s) {
   if (!q) return adam_v<PT, GT, MT, kNoCopy>(a, count, p, g, m, v, q, qs, amax, cap, s);
   if (qt == E5MA_E5M2) return adam_v<PT, GT, MT, E5MA_E5M2>(a, count, p, g, m, v, q, qs, amax, cap, s);
@@ -122,14 +124,14 @@ hipError_t adam_q(int qt, const AdamScalars &a, size_t count, void *p, const voi
 }
 
 template <int PT, int GT>
-hipError_t adam_m(int mt, int qt, const AdamScalars &a, size_t count, void *p, const void *g, void *m, void *v,
+hipError_t adam_m(int mt, int qt, const AdamCoefficients &a, size_t count, void *p, const void *g, void *m, void *v,
                   uint8_t *q, const float *qs, float *amax, int cap, hipStream_t s) {
   if (mt == E5MA_BF16) return adam_q<PT, GT, E5MA_BF16>(qt, a, count, p, g, m, v, q, qs, amax, cap, s);
   return adam_q<PT, GT, E5MA_FP32>(qt, a, count, p, g, m, v, q, qs, amax, cap, s);
 }
 
 template <int PT>
-hipError_t adam_g(int gt, int mt, int qt, const AdamScalars &a, size_t count, void *p, const void *g, void *m,
+hipError_t adam_g(int gt, int mt, int qt, const AdamCoefficients &a, size_t count, void *p, const void *g, void *m,
                   void *v, uint8_t *q, const float *qs, float *amax, int cap, hipStream_t s) {
   if (gt == E5MA_BF16) return adam_m<PT, E5MA_BF16>(mt, qt, a, count, p, g, m, v, q, qs, amax, cap, s);
   if (gt == E5MA_FP16) return adam_m<PT, E5MA_FP16>(mt, qt, a, count, p, g, m, v, q, qs, amax, cap, s);
@@ -138,7 +140,7 @@ hipError_t adam_g(int gt, int mt, int qt, const AdamScalars &a, size_t count, vo
 
 }  // namespace
 
-hipError_t launch_adam(const AdamScalars &a, size_t count, int pt, void *p, int gt, const void *g, int mt, void *m,
+hipError_t launch_adam(const AdamCoefficients &a, size_t count, int pt, void *p, int gt, const void *g, int mt, void *m,
                        void *v, int qt, uint8_t *q, const float *qscale, float *amax, const Tuning &t,
                        hipStream_t s) {
   const int cap = pt == E5MA_BF16 ? t.adam_grid_bf16 : t.adam_grid_fp32;

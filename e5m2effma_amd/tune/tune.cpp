@@ -17,7 +17,7 @@
 //                   call, its cast pass at the cast_grid just chosen), same sources
 //   adam_grid_*     AdamW over 2^28 parameters, BF16 resp. FP32 state, with an E5M2 copy
 //   splitk_div      E5M2 x E5M2 -> BF16 TN GEMMs with at most 64 tiles: 512^2, 1024^2, 2048^2, 4096 x 1024
-//                   and 8192 x 64, all with k = 8192 (summed)
+//                   and 8192 x 64, all with k = 8192 (summed), given a full workspace (e5ma_gemm_ex)
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdio.h>
@@ -166,9 +166,9 @@ static Tuning tune_device(const DeviceInfo &di) {
     const size_t n = (size_t)1 << 28, es = pt == E5MA_BF16 ? 2 : 4;
     void *p = dalloc(n * es, 0x3C), *g = dalloc(n * es, 0x3A), *m = dalloc(n * es, 0x38), *v = dalloc(n * es, 0x30);
     uint8_t *q = (uint8_t *)dalloc(n, 0);
-    AdamScalars a{};
-    a.lr = 1e-4f; a.beta1 = 0.9f; a.beta2 = 0.999f; a.omb1 = 0.1f; a.omb2 = 0.001f; a.rbc1 = 1.f; a.rbc2 = 1.f;
-    a.eps = 1e-8f; a.lr_wd = 1e-6f; a.wd = 0.01f; a.gscale = 1.f; a.adamw = 1;
+    AdamCoefficients a{};
+    a.lr = 1e-4f; a.b1 = 0.9f; a.b2 = 0.999f; a.c1 = 0.1f; a.c2 = 0.001f; a.corr1 = 1.f; a.corr2 = 1.f;
+    a.eps = 1e-8f; a.decay = 1e-6f; a.l2 = 0.01f; a.grad_mul = 1.f; a.decoupled = 1;
     const std::vector<int> cands = pt == E5MA_BF16 ? std::vector<int>{16384, 32768, 65536, 131072}
                                                    : std::vector<int>{4096, 8192, 16384, 32768};
     std::vector<float> ms;
@@ -189,6 +189,7 @@ static Tuning tune_device(const DeviceInfo &di) {
     const size_t big = (size_t)8192 * 8192;
     uint8_t *A = (uint8_t *)dalloc(big, 0x33), *B = (uint8_t *)dalloc(big, 0x35);
     void *D = dalloc(big * 2, 0);
+    const Workspace ws{dalloc(kMaxWorkspace, 0), kMaxWorkspace};  // as e5ma_gemm_ex is given
     const std::vector<int> cands = {0, 2, 4, 8};
     std::vector<float> ms;
     for (int c : cands) {
@@ -204,13 +205,13 @@ static Tuning tune_device(const DeviceInfo &di) {
         e.d_dtype = E5MA_BF16;
         e.c_dtype = E5MA_FP32;
         e.bias_dtype = E5MA_FP32;
-        sum += best_ms([&](int) { return launch_gemm(E5MA_E5M2, E5MA_E5M2, true, true, A, s.k, B, s.k, s.m, s.n, s.k, e, x, nullptr); }, 5);
+        sum += best_ms([&](int) { return launch_gemm(E5MA_E5M2, E5MA_E5M2, true, true, A, s.k, B, s.k, s.m, s.n, s.k, e, x, ws, nullptr); }, 5);
       }
       ms.push_back(sum);
     }
     printf("GEMM TN E5M2 x E5M2 -> BF16, k = 8192, m x n in {512^2, 1024^2, 2048^2, 4096 x 1024, 8192 x 64} (summed)\n");
     t.splitk_div = pick("splitk_div", cands, ms, def.splitk_div);
-    for (void *b : {(void *)A, (void *)B, D}) check(hipFree(b), "hipFree");
+    for (void *b : {(void *)A, (void *)B, D, ws.ptr}) check(hipFree(b), "hipFree");
   }
   printf("outputs of %d cast / quantize candidates compared with their first candidate's: %d differ\n", checked,
          differing);
@@ -269,9 +270,13 @@ int main(int argc, char **argv) {
     else path = argv[i];
   }
   check(hipSetDevice(0), "hipSetDevice");
-  if (e5ma_status st = check_device()) {
-    fprintf(stderr, "device 0 is not supported (status %d)\n", (int)st);
-    return 1;
+  {
+    Call call;
+    int dev = 0;
+    if (e5ma_status st = resolve_device(call, &dev)) {
+      fprintf(stderr, "device 0 is not supported (status %d): %s\n", (int)st, thread_message());
+      return 1;
+    }
   }
   const DeviceInfo &di = device_info(0);
   hipDeviceProp_t p;

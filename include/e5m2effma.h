@@ -70,7 +70,10 @@ typedef struct {
   e5ma_scaling scaling;    /* FP8 GEMM operands only: E5MA_SCALING_OUTER = scale_inv vector */
 } e5ma_tensor;
 
-/* Replaces reference e5ma_gemm (include/e5m2effma.h:73-76, src/gemm_e5m2effma.cu:44-104). */
+/* Replaces reference e5ma_gemm (include/e5m2effma.h:73-76, src/gemm_e5m2effma.cu:44-104).  Like the
+ * reference it allocates and uses no device memory beyond its arguments, and it gives the same bits on
+ * every MI355X for the same inputs (e5ma_gemm_ex in e5m2effma_ext.h adds split-K with a caller-owned
+ * workspace). */
 e5ma_status e5ma_gemm(e5ma_op transa, e5ma_op transb, int m, int n, int k, float alpha,
                       const e5ma_tensor *A, int lda, const e5ma_tensor *B, int ldb, float beta,
                       const e5ma_tensor *C, int ldc, const e5ma_tensor *D, int ldd,

@@ -111,8 +111,15 @@ class GemmCase:
                         ocp_operands=True)
         return g
 
-    def run(self, dev, stream=None):
-        """Run on the GPU; returns (status, D as numpy, amax or None)."""
+    def workspace_bytes(self):
+        """e5ma_gemm_workspace_size for this call on the current device."""
+        return _lib.workspace_size(self.transa, self.transb, self.m, self.n, self.k, self.adt, self.lda, self.bdt,
+                                   self.ldb)
+
+    def run(self, dev, stream=None, workspace=None):
+        """Run on the GPU; returns (status, D as numpy, amax or None).  workspace: None runs e5ma_gemm;
+        a byte count runs e5ma_gemm_ex with a fresh device workspace of that size ("query": the size
+        e5ma_gemm_workspace_size reports)."""
         keep = []
 
         def put(a):
@@ -142,9 +149,15 @@ class GemmCase:
         bias = _lib.tensor(pbias, self.biasdt) if self.bias is not None else None
         st = ctypes.c_void_p(stream if stream is not None else torch.cuda.current_stream(dev).cuda_stream)
         L = _lib.lib()
-        s = L.e5ma_gemm(self.transa, self.transb, self.m, self.n, self.k, float(self.alpha), _lib.ref(A), self.lda,
-                        _lib.ref(B), self.ldb, float(self.beta), _lib.ref(C), self.ldc, _lib.ref(D), self.ldd,
-                        _lib.ref(bias), st)
+        args = (self.transa, self.transb, self.m, self.n, self.k, float(self.alpha), _lib.ref(A), self.lda,
+                _lib.ref(B), self.ldb, float(self.beta), _lib.ref(C), self.ldc, _lib.ref(D), self.ldd, _lib.ref(bias))
+        if workspace is None:
+            s = L.e5ma_gemm(*args, st)
+        else:
+            nbytes = self.workspace_bytes() if workspace == "query" else int(workspace)
+            ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
+            keep.append(ws)
+            s = L.e5ma_gemm_ex(*args, ws.data_ptr() if nbytes else None, nbytes, st)
         torch.cuda.synchronize(dev)
         D_got = from_dev(Dt, pd, NPD[self.ddt], self.ldd * self.n)
         return s, D_got, (None if am_t is None else float(am_t.item()))

@@ -157,3 +157,23 @@ def test_no_device_is_a_runtime_error():
         pytest.skip("a GPU is present")
     s, err = gemm()
     assert s == 3 and err.startswith("hipGetDevice: HIP error")
+
+
+def test_gemm_ex_and_workspace_query_validation():
+    """e5ma_gemm_ex checks its workspace first, then runs e5ma_gemm's rules with its own name;
+    e5ma_gemm_workspace_size checks its arguments before any device use."""
+    L = _lib.lib()
+    A, B, D = T(), T(), T(BF16)
+    ex = lambda ws, nbytes, k=32: (L.e5ma_gemm_ex(1, 0, 32, 32, k, 1.0, _lib.ref(A), 32, _lib.ref(B), 32, 0.0, None, 0,
+                                                  _lib.ref(D), 32, None, ws, nbytes, None), _lib.last_error())
+    assert ex(FAKE + 16, 4096) == (1, "e5ma_gemm_ex: a workspace of 4096 bytes needs a 256-byte aligned pointer")
+    assert ex(None, 4096) == (1, "e5ma_gemm_ex: a workspace of 4096 bytes needs a 256-byte aligned pointer")
+    assert ex(FAKE, 4096, k=24) == (1, "e5ma_gemm_ex: k = 24 is not a multiple of 16")
+    assert ex(None, 0, k=24) == (1, "e5ma_gemm_ex: k = 24 is not a multiple of 16")
+    out = ctypes.c_size_t(7)
+    ws = lambda *a: (L.e5ma_gemm_workspace_size(*a), _lib.last_error())
+    assert ws(1, 0, 32, 32, 32, E5M2, 32, E5M2, 32, None) == (1, "e5ma_gemm_workspace_size: bytes is NULL")
+    assert ws(2, 0, 32, 32, 32, E5M2, 32, E5M2, 32, ctypes.byref(out))[0] == 1
+    assert ws(1, 0, 32, 32, 32, FP16, 32, E5M2, 32, ctypes.byref(out))[0] == 2
+    assert ws(1, 0, 0, 32, 32, E5M2, 32, E5M2, 32, ctypes.byref(out)) == (0, "") and out.value == 0
+    assert ws(1, 0, 32, 4, 32, E5M2, 32, BF16, 32, ctypes.byref(out)) == (0, "") and out.value == 0  # GEMV route

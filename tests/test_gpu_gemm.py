@@ -353,9 +353,10 @@ def test_h_config3_fp8_x_bf16_sampled(dev):
     assert bad == 0, first
 
 
-# ---- split-K: outputs with at most half as many 256 x 256 tiles as CUs split K into FP32 partials that
-# a reduce kernel sums in order and runs through the epilogue (most fast-kernel tests above are such
-# shapes); these check the unsplit kernels (more than 128 tiles) and split counts at the edges ---------
+# ---- split-K (e5ma_gemm_ex with a caller workspace): outputs with at most a quarter as many 256 x 256
+# tiles as CUs split K into FP32 partials that a reduce kernel sums in order and runs through the
+# epilogue; e5ma_gemm never splits.  These check the unsplit kernels (more than 64 tiles) and split
+# counts at the edges ---------------------------------------------------------------------------------
 @pytest.mark.parametrize("ta,tb", [(1, 0), (0, 0)])
 def test_fast_unsplit_f8_sampled(dev, ta, tb):
     rng = np.random.default_rng(9700 + ta * 2 + tb)
@@ -381,14 +382,49 @@ def test_fast_unsplit_h_sampled(dev):
                                             (1024, 8192, 8192, E5, E5), (64, 48, 512, E5, E4),
                                             (130, 20, 768, E4, B16)])
 def test_splitk_shapes(dev, m, n, k, adt, bdt):
-    """Skinny, tiny and half-filled grids (split counts 8, 32, 2, 1 and 3), FP8 output with amax."""
+    """Skinny, tiny and half-filled grids through e5ma_gemm_ex with the workspace it asks for (split
+    counts 8, 32, 1, 1 and 3 on 256 CUs), FP8 output with amax."""
     rng = np.random.default_rng(m + n + k)
     case = gu.GemmCase(rng, 1, 0, m, n, k, adt, bdt, ddt=E5, qscale=0.5, amax=True, dist="normal", sigma=2.0,
                        sa=0.25, pad=0 if m * n > 10**6 else 16)
-    s, D, amax = case.run(dev)
+    s, D, amax = case.run(dev, workspace="query")
     assert s == 0
     bad, first = case.check(D, amax, samples=4096 if m * n > 10**6 else None, rng=rng)
     assert bad == 0, first
+
+
+@pytest.mark.parametrize("m,n,k,adt,bdt,ta,tb", [(2048, 2048, 8192, E5, E4, 1, 0), (512, 768, 16384, E4, E5, 0, 1),
+                                                  (1024, 512, 2048, E5, B16, 1, 0)])
+def test_split_and_unsplit_both_in_bound(dev, m, n, k, adt, bdt, ta, tb):
+    """The same GEMM unsplit (e5ma_gemm), split with the full workspace (e5ma_gemm_ex) and split fewer
+    ways with a quarter of it: every result inside the oracle bound; a split sums the products in another
+    order, so the bits may differ from the unsplit result's (they are not compared); the same split
+    count gives the same bits on a repeat call (deterministic reduction)."""
+    rng = np.random.default_rng(m + n + 3 * k)
+    case = gu.GemmCase(rng, ta, tb, m, n, k, adt, bdt, ddt=F32, alpha=0.5, sa=0.25, biasdt=F32, beta=-0.5,
+                       cdt=B16, dist="normal", sigma=2.0, pad=0)
+    full = case.workspace_bytes()
+    assert full > 0, "this shape splits K on a 256-CU device"
+    results = []
+    for ws in (None, full, full // 4):
+        s, D, _ = case.run(dev, workspace=ws)
+        assert s == 0
+        bad, first = case.check(D, samples=4096, rng=rng)
+        assert bad == 0, (ws, first)
+        results.append(D)
+    s, D2, _ = case.run(dev, workspace=full)
+    assert s == 0 and np.array_equal(D2.view(np.uint32), results[1].view(np.uint32))
+
+
+def test_workspace_query_matches_rule(dev):
+    """e5ma_gemm_workspace_size: 0 for grids that fill more than a quarter of the CUs, for GEMV-routed
+    calls and for the generic kernel; S * ldw * n * 4 bytes (ldw = m rounded up to 4) otherwise."""
+    q = lambda ta, tb, m, n, k, a, b: gu._lib.workspace_size(ta, tb, m, n, k, a, k if ta else m, b, n if tb else k)
+    assert q(1, 0, 8192, 8192, 8192, E5, E4) == 0
+    assert q(1, 0, 8192, 4, 8192, E5, B16) == 0            # GEMV
+    assert q(1, 0, 64, 64, 64, F32, F32) == 0              # generic kernel
+    b = q(1, 0, 2048, 2048, 8192, E5, E4)
+    assert b > 0 and b % (2048 * 2048 * 4) == 0 and b <= 64 << 20
 
 
 def test_direct_epilogue_bf16_nan_codes(dev):
