@@ -16,7 +16,7 @@ SCALING_TENSOR, SCALING_OUTER = 0, 1
 
 # every symbol include/e5m2effma.h and include/e5m2effma_ext.h declare
 EXPORTS = ("e5ma_gemm", "e5ma_cast", "e5ma_adam", "e5ma_status_string", "e5ma_last_error", "e5ma_quantize",
-           "e5ma_gemm_ex", "e5ma_gemm_workspace_size")
+           "e5ma_gemm_ex", "e5ma_gemm_workspace_size", "e5ma_gemm_noalloc")
 
 
 class Tensor(ctypes.Structure):
@@ -49,6 +49,8 @@ def lib():
         L.e5ma_gemm.argtypes = [I, I, I, I, I, F, TP, I, TP, I, F, TP, I, TP, I, TP, P]
         L.e5ma_gemm_ex.restype = I
         L.e5ma_gemm_ex.argtypes = [I, I, I, I, I, F, TP, I, TP, I, F, TP, I, TP, I, TP, P, S, P]
+        L.e5ma_gemm_noalloc.restype = I
+        L.e5ma_gemm_noalloc.argtypes = [I, I, I, I, I, F, TP, I, TP, I, F, TP, I, TP, I, TP, P]
         L.e5ma_gemm_workspace_size.restype = I
         L.e5ma_gemm_workspace_size.argtypes = [I, I, I, I, I, I, I, I, I, ctypes.POINTER(S)]
         L.e5ma_cast.restype = I

@@ -153,7 +153,7 @@ bool routes_to_gemv(int n, bool akc, bool bkc, int at) { return n <= 8 && akc &&
 e5ma_status gemm_entry(const char *name, e5ma_op transa, e5ma_op transb, int m, int n, int k, float alpha,
                        const e5ma_tensor *A, int lda, const e5ma_tensor *B, int ldb, float beta,
                        const e5ma_tensor *C, int ldc, const e5ma_tensor *D, int ldd, const e5ma_tensor *bias,
-                       const Workspace &ws, hipStream_t stream) {
+                       const WorkspaceSource &src, hipStream_t stream) {
   Call call;
   const bool reads_c = beta != 0.f && has_data(C);
   call.need(has_data(A) && has_data(B) && has_data(D), E5MA_INVALID_VALUE, "%s: A, B, D or their data is NULL", name)
@@ -191,9 +191,19 @@ e5ma_status gemm_entry(const char *name, e5ma_op transa, e5ma_op transb, int m, 
             E5MA_INVALID_VALUE, "%s: C, D and bias take per-tensor scaling only", name);
   int dev = 0;
   if (!call.ok() || resolve_device(call, &dev)) return call.status();
+  const DeviceInfo &di = device_info(dev);
+  const Workspace ws = src.per_device ? src.per_device(dev, call) : src.given;
+  if (src.per_device && call.ok()) {
+    const size_t want = routes_to_gemv(n, akc, bkc, A->dtype)
+                            ? 0
+                            : gemm_workspace_bytes(A->dtype, B->dtype, akc, bkc, m, n, k, lda, ldb, di);
+    call.need(want <= ws.bytes, E5MA_INVALID_VALUE,
+              "%s: this GEMM's split-K partials need %zu bytes, more than the library's scratch of %zu bytes", name,
+              want, ws.bytes);
+  }
+  if (!call.ok()) return call.status();
 
   const dev::Epilogue e = epilogue_of(alpha, A, B, beta, C, ldc, D, ldd, bias);
-  const DeviceInfo &di = device_info(dev);
   const uint8_t *a = (const uint8_t *)A->data, *b = (const uint8_t *)B->data;
   const hipError_t err = routes_to_gemv(n, akc, bkc, A->dtype)
                              ? launch_gemv(A->dtype, B->dtype, a, lda, b, ldb, m, n, k, e, di, stream)
@@ -328,7 +338,7 @@ extern "C" e5ma_status e5ma_gemm(e5ma_op transa, e5ma_op transb, int m, int n, i
                                  const e5ma_tensor *C, int ldc, const e5ma_tensor *D, int ldd,
                                  const e5ma_tensor *bias, hipStream_t stream) {
   return e5ma::gemm_entry("e5ma_gemm", transa, transb, m, n, k, alpha, A, lda, B, ldb, beta, C, ldc, D, ldd, bias,
-                          e5ma::Workspace{}, stream);
+                          e5ma::WorkspaceSource{}, stream);
 }
 
 // e5ma_gemm with a caller-owned split-K workspace (include/e5m2effma_ext.h)
@@ -343,8 +353,10 @@ extern "C" e5ma_status e5ma_gemm_ex(e5ma_op transa, e5ma_op transb, int m, int n
               "e5ma_gemm_ex: a workspace of %zu bytes needs a 256-byte aligned pointer", workspace_bytes);
     if (!call.ok()) return call.status();
   }
+  e5ma::WorkspaceSource src;
+  src.given = e5ma::Workspace{workspace_bytes ? workspace : nullptr, workspace_bytes};
   return e5ma::gemm_entry("e5ma_gemm_ex", transa, transb, m, n, k, alpha, A, lda, B, ldb, beta, C, ldc, D, ldd, bias,
-                          e5ma::Workspace{workspace_bytes ? workspace : nullptr, workspace_bytes}, stream);
+                          src, stream);
 }
 
 extern "C" e5ma_status e5ma_gemm_workspace_size(e5ma_op transa, e5ma_op transb, int m, int n, int k,

@@ -108,9 +108,18 @@ size_t gemm_workspace_bytes(int at, int bt, bool akc, bool bkc, int m, int n, in
                             const DeviceInfo &di);
 
 // ---- e5ma_gemm's request, shared by every GEMM entry point (api.cpp) ----------------------------
+// Where a GEMM's split-K workspace comes from: memory the caller gave (or none), or, when per_device is
+// set, a function that returns device dev's memory once the arguments have passed their rules and dev
+// is the current device (it reports a failure through call).
+// A per-device workspace has a fixed capacity: a call whose split-K partials would need more is
+// rejected (the caller's workspace of e5ma_gemm_ex instead limits the split count).
+struct WorkspaceSource {
+  Workspace given;
+  Workspace (*per_device)(int dev, Call &call) = nullptr;
+};
 e5ma_status gemm_entry(const char *name, e5ma_op transa, e5ma_op transb, int m, int n, int k, float alpha,
                        const e5ma_tensor *A, int lda, const e5ma_tensor *B, int ldb, float beta,
                        const e5ma_tensor *C, int ldc, const e5ma_tensor *D, int ldd, const e5ma_tensor *bias,
-                       const Workspace &ws, hipStream_t stream);
+                       const WorkspaceSource &src, hipStream_t stream);
 
 }  // namespace e5ma

@@ -7,6 +7,7 @@
  *                             e5ma_cast in Float8Tensor.from_float (binds/python/e5m2effma/tensor.py:52-74)
  *   e5ma_gemm_ex              e5ma_gemm with a caller-owned workspace for split-K on small grids
  *   e5ma_gemm_workspace_size  the workspace e5ma_gemm_ex uses for a shape
+ *   e5ma_gemm_noalloc         e5ma_gemm_ex on the library's fixed per-device scratch: allocates nothing
  */
 #ifndef E5M2EFFMA_EXT_H
 #define E5M2EFFMA_EXT_H
@@ -56,6 +57,19 @@ e5ma_status e5ma_gemm_ex(e5ma_op transa, e5ma_op transb, int m, int n, int k, fl
 e5ma_status e5ma_gemm_workspace_size(e5ma_op transa, e5ma_op transb, int m, int n, int k,
                                      e5ma_dtype a_dtype, int lda, e5ma_dtype b_dtype, int ldb,
                                      size_t *bytes);
+
+/* No counterpart in the reference: for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  e5ma_gemm_ex with the library's own
+ * scratch as the workspace: a fixed 64 MiB per device (the largest workspace any GEMM asks for), a
+ * file-scope device array reserved when the library loads on a device and held until the process ends.
+ * The call allocates nothing.  Same results as e5ma_gemm_ex given e5ma_gemm_workspace_size()'s bytes; a
+ * call whose split-K partials would need more than the scratch is rejected with E5MA_INVALID_VALUE (none
+ * does with 64 MiB).  Every call on a device shares that device's scratch: calls whose work overlaps on
+ * one device (unordered streams) race on it and must not be issued. */
+e5ma_status e5ma_gemm_noalloc(e5ma_op transa, e5ma_op transb, int m, int n, int k, float alpha,
+                              const e5ma_tensor *A, int lda, const e5ma_tensor *B, int ldb, float beta,
+                              const e5ma_tensor *C, int ldc, const e5ma_tensor *D, int ldd,
+                              const e5ma_tensor *bias, hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -177,3 +177,14 @@ def test_gemm_ex_and_workspace_query_validation():
     assert ws(1, 0, 32, 32, 32, FP16, 32, E5M2, 32, ctypes.byref(out))[0] == 2
     assert ws(1, 0, 0, 32, 32, E5M2, 32, E5M2, 32, ctypes.byref(out)) == (0, "") and out.value == 0
     assert ws(1, 0, 32, 4, 32, E5M2, 32, BF16, 32, ctypes.byref(out)) == (0, "") and out.value == 0  # GEMV route
+
+
+def test_gemm_noalloc_validation():
+    """e5ma_gemm_noalloc runs e5ma_gemm's rules, with its own name, before any device use."""
+    L = _lib.lib()
+    A, B, D = T(), T(), T(BF16)
+    na = lambda k=32, m=32: (L.e5ma_gemm_noalloc(1, 0, m, 32, k, 1.0, _lib.ref(A), 32, _lib.ref(B), 32, 0.0, None, 0,
+                                                 _lib.ref(D), 32, None, None), _lib.last_error())
+    assert na(k=24) == (1, "e5ma_gemm_noalloc: k = 24 is not a multiple of 16")
+    assert na(m=-1) == (1, "e5ma_gemm_noalloc: negative size (m=-1 n=32 k=32)")
+    assert na(m=0) == (0, "")
