@@ -263,7 +263,7 @@ __device__ __forceinline__ void k_loop(const Loads<true> &L, int nk, int lane, i
   f8_unit<true, 1, false, 0, 0, false, 0, 0, false, 0, AT, BT, AKC, BKC>(L, 0, lane, wm, wn, a, b, acc);
 }
 
-template <int AT, int BT, int DT, bool AKC, bool BKC>
+template <int AT, int BT, bool AKC, bool BKC, int EPI>
 __global__ __launch_bounds__(kThreads, 1) void gemm_f8_kernel(TileArgs t, Epilogue e, int simple, int vec) {
   constexpr bool PAIR = BKC;  // the ring shape measured faster for this layout
   __shared__ float red[kThreads / 64];
@@ -273,6 +273,9 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_f8_kernel(TileArgs t, Epilog
   tile_of(blockIdx.x, t, tm, tn, sp);
   apply_split(t, e, sp);
   const int i0 = tm * kBM, j0 = tn * kBN;
+
+  float sa1, sb1;
+  epilogue_scales(e, sa1, sb1);
 
   v16f acc[4][4];
 #pragma unroll
@@ -285,27 +288,22 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_f8_kernel(TileArgs t, Epilog
   const Loads<PAIR> L = make_loads<AKC, BKC, PAIR>(t, i0, j0, wave, lane);
   k_loop<AT, BT, AKC, BKC>(L, t.k / kUnitK, lane, wm, wn, a, b, acc);
 
-  const float mx = tile_epilogue<DT>(t, e, acc, i0, j0, wm, wn, lane, tid, simple, vec);
+  const float mx = tile_epilogue<EPI>(t, e, acc, i0, j0, wm, wn, lane, tid, simple, vec, sa1, sb1);
   if (e.amax) amax_commit_block(e.amax, mx, red);
 }
 
 template <int AT, int BT, bool AKC, bool BKC>
 hipError_t run_d(const TileArgs &t, const Epilogue &e, hipStream_t s) {
   const int grid = t.tiles_m * t.tiles_n * t.splits;
-  // the direct epilogue needs 4-element-aligned D columns and, with OUTER scaling of A, a 16-byte
-  // aligned scale vector
+  // the staged epilogues write 4-element groups of D and read OUTER scales of A as 16-byte vectors
   const int vec = ((uintptr_t)e.d % (4 * elem_bytes(e.d_dtype))) == 0 && e.ldd % 4 == 0 &&
                   (!e.sa_vec || (uintptr_t)e.sa % 16 == 0);
   const int simple = e.bias == nullptr && e.beta == 0.f && vec;
-#define E5MA_F8(DT) gemm_f8_kernel<AT, BT, DT, AKC, BKC><<<grid, kThreads, 0, s>>>(t, e, simple, vec)
-  switch (e.d_dtype) {
-    case E5MA_BF16: E5MA_F8(E5MA_BF16); break;
-    case E5MA_FP16: E5MA_F8(E5MA_FP16); break;
-    case E5MA_FP32: E5MA_F8(E5MA_FP32); break;
-    case E5MA_E5M2: E5MA_F8(E5MA_E5M2); break;
-    default: E5MA_F8(E5MA_E4M3); break;
+  switch (epilogue_class(t.m, t.n, e, simple, vec)) {  // D's dtype is a run-time choice of the epilogue
+    case kEpiFast16: gemm_f8_kernel<AT, BT, AKC, BKC, kEpiFast16><<<grid, kThreads, 0, s>>>(t, e, simple, vec); break;
+    case kEpiFull: gemm_f8_kernel<AT, BT, AKC, BKC, kEpiFull><<<grid, kThreads, 0, s>>>(t, e, simple, vec); break;
+    default: gemm_f8_kernel<AT, BT, AKC, BKC, kEpiAny><<<grid, kThreads, 0, s>>>(t, e, simple, vec); break;
   }
-#undef E5MA_F8
   return hipGetLastError();
 }
 

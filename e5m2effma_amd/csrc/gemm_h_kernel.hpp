@@ -182,7 +182,7 @@ __device__ __forceinline__ void h_stage(const TileArgs &t, int s, int i0, int j0
   }
 }
 
-template <int AT, int BT, int DT, bool AKC, bool BKC>
+template <int AT, int BT, bool AKC, bool BKC, int EPI>
 __global__ __launch_bounds__(kThreads, 1) void gemm_h_kernel(TileArgs t, Epilogue e, int simple, int vec) {
   using C = Cfg<AT, BT, AKC, BKC>;
   __shared__ float red[kThreads / 64];
@@ -193,6 +193,9 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_h_kernel(TileArgs t, Epilogu
   apply_split(t, e, sp);
   const int i0 = tm * kBM, j0 = tn * kBN;
   const int nk = t.k / C::KS;
+
+  float sa1, sb1;
+  epilogue_scales(e, sa1, sb1);
 
   v16f acc[4][4];
 #pragma unroll
@@ -232,7 +235,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_h_kernel(TileArgs t, Epilogu
   h_stage<C, 0, true, false, 2, AT, BT, AKC, BKC>(t, s + 2, i0, j0, wave, lane, wm, wn, a, b, acc);
   h_stage<C, 0, false, false, 3, AT, BT, AKC, BKC>(t, s + 3, i0, j0, wave, lane, wm, wn, a, b, acc);
 
-  const float mx = tile_epilogue<DT>(t, e, acc, i0, j0, wm, wn, lane, tid, simple, vec);
+  const float mx = tile_epilogue<EPI>(t, e, acc, i0, j0, wm, wn, lane, tid, simple, vec, sa1, sb1);
   if (e.amax) amax_commit_block(e.amax, mx, red);
 }
 
@@ -242,15 +245,11 @@ hipError_t run_d(const TileArgs &t, const Epilogue &e, hipStream_t s) {
   const int vec = ((uintptr_t)e.d % (4 * elem_bytes(e.d_dtype))) == 0 && e.ldd % 4 == 0 &&
                   (!e.sa_vec || (uintptr_t)e.sa % 16 == 0);
   const int simple = e.bias == nullptr && e.beta == 0.f && vec;
-#define E5MA_H(DT) gemm_h_kernel<AT, BT, DT, AKC, BKC><<<grid, kThreads, 0, s>>>(t, e, simple, vec)
-  switch (e.d_dtype) {
-    case E5MA_BF16: E5MA_H(E5MA_BF16); break;
-    case E5MA_FP16: E5MA_H(E5MA_FP16); break;
-    case E5MA_FP32: E5MA_H(E5MA_FP32); break;
-    case E5MA_E5M2: E5MA_H(E5MA_E5M2); break;
-    default: E5MA_H(E5MA_E4M3); break;
+  switch (epilogue_class(t.m, t.n, e, simple, vec)) {  // D's dtype is a run-time choice of the epilogue
+    case kEpiFast16: gemm_h_kernel<AT, BT, AKC, BKC, kEpiFast16><<<grid, kThreads, 0, s>>>(t, e, simple, vec); break;
+    case kEpiFull: gemm_h_kernel<AT, BT, AKC, BKC, kEpiFull><<<grid, kThreads, 0, s>>>(t, e, simple, vec); break;
+    default: gemm_h_kernel<AT, BT, AKC, BKC, kEpiAny><<<grid, kThreads, 0, s>>>(t, e, simple, vec); break;
   }
-#undef E5MA_H
   return hipGetLastError();
 }
 

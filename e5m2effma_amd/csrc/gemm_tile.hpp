@@ -1,6 +1,7 @@
 // gemm_tile.hpp -- what the matrix-core tile kernels (gemm_f8_kernel.hpp, gemm_h_kernel.hpp) share:
 // the 256 x 256 block tile of 4 waves (128 x 128 accumulators each, 4 x 4 blocks of 32 x 32), the
-// 128 KiB LDS ring of 8 buffers and its direct-to-LDS loads, the XCD-aware tile order, and the epilogue.
+// 128 KiB LDS ring of 8 buffers and its direct-to-LDS loads, the XCD-aware tile order, and the
+// epilogues, which stage the finished tile in the ring.
 #pragma once
 #include "e5ma_host.hpp"
 #include "gemm_common.hpp"
@@ -152,6 +153,9 @@ template <int T> __device__ __forceinline__ void load4_t(const void *p, size_t i
 // per column when C is aligned) before any is computed or stored, so 32 values per thread are in
 // flight (C may alias D: each element is read before it is written, by the same thread).  CT: the
 // dtype of C, or -1 when beta = 0.
+// C's / D's dtype chosen at run time, element by element (the common pairings have their own instances)
+constexpr int kAnyC = 100, kAnyD = 101;
+
 template <int DT, int CT>
 __device__ __forceinline__ float general_half(const Epilogue &e, const EpiState &st, const TileArgs &t, int i, int jh,
                                               const float (&rs)[4], const float (&rb)[4], int vec, int tid,
@@ -160,7 +164,7 @@ __device__ __forceinline__ float general_half(const Epilogue &e, const EpiState 
   const int w = tid >> 6, il = 4 * (tid & 63);
   const bool rows4 = i + 3 < t.m;
   bool cvec = false;
-  if constexpr (CT >= 0)
+  if constexpr (CT >= 0 && CT != kAnyC)
     cvec = rows4 && (uintptr_t)e.c % (4 * elem_bytes(CT)) == 0 && e.ldc % 4 == 0;
   const float sb1 = scale_or_one(e.sb);
 #pragma unroll 1
@@ -173,7 +177,13 @@ __device__ __forceinline__ float general_half(const Epilogue &e, const EpiState 
       a[u][0] = v4.x; a[u][1] = v4.y; a[u][2] = v4.z; a[u][3] = v4.w;
 #pragma unroll
       for (int q = 0; q < 4; ++q) cv[u][q] = 0.f;
-      if constexpr (CT >= 0) {
+      if constexpr (CT == kAnyC) {
+        if (j < t.n && e.beta != 0.f) {  // beta = 0: there is no C (NULL), and none is read
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            if (i + q < t.m) cv[u][q] = load_any(e.c_dtype, e.c, (size_t)j * e.ldc + i + q, st.csinv);
+        }
+      } else if constexpr (CT >= 0) {
         if (j < t.n) {
           if (cvec) {
             load4_t<CT>(e.c, (size_t)j * e.ldc + i, st.csinv, cv[u]);
@@ -195,10 +205,22 @@ __device__ __forceinline__ float general_half(const Epilogue &e, const EpiState 
       for (int q = 0; q < 4; ++q) {
         v[q] = a[u][q] * ((e.sa_vec || e.sb_vec) ? rs[q] * sbj : st.s);
         if (e.bias) v[q] = v[q] + rb[q];
-        if constexpr (CT >= 0) v[q] = __builtin_fmaf(e.beta, cv[u][q], v[q]);
+        if constexpr (CT == kAnyC) {
+          if (e.beta != 0.f) v[q] = __builtin_fmaf(e.beta, cv[u][q], v[q]);
+        } else if constexpr (CT != -1) {
+          v[q] = __builtin_fmaf(e.beta, cv[u][q], v[q]);
+        }
       }
       const size_t o = (size_t)j * e.ldd + i;
-      if (rows4 && vec) {
+      if constexpr (DT == kAnyD) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          if (i + q < t.m) {
+            store_any(e.d_dtype, e.d, o + q, v[q], st.qscale);
+            mx = amax_fold(mx, v[q]);
+          }
+        continue;
+      } else if (rows4 && vec) {
         uint8_t *dp = (uint8_t *)e.d + o * elem_bytes(DT);
         if constexpr (DT == E5MA_FP32) {
           *(float4 *)dp = make_float4(v[0], v[1], v[2], v[3]);
@@ -224,223 +246,338 @@ __device__ __forceinline__ float general_half(const Epilogue &e, const EpiState 
   return mx;
 }
 
-// Four BF16 codes (v[0] in the lowest half) by the hardware's pair conversion v_cvt_pk_bf16_f32: checked
-// here against the integer round-to-nearest-even encoder over all 2^32 FP32 inputs, identical except for
-// NaNs, which it keeps NaN but with their sign and payload.  Every NaN must become 0x7FC0
-// (include/e5m2effma.h, reference rne_hi), so lanes holding one take a rarely executed fix-up: the
-// common path is 4 compares and 2 conversions per 4 values (the integer encoder costs about 6 per value).
-__device__ __forceinline__ uint2 bf16_quad(const float (&v)[4]) {
-  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-  uint32_t lo = __builtin_bit_cast(uint32_t, bf16x2_t{(__bf16)v[0], (__bf16)v[1]});
-  uint32_t hi = __builtin_bit_cast(uint32_t, bf16x2_t{(__bf16)v[2], (__bf16)v[3]});
-  // the flags are taken before the branch, so the values are dead across it (else they are spilled)
-  const bool n0 = v[0] != v[0], n1 = v[1] != v[1], n2 = v[2] != v[2], n3 = v[3] != v[3];
-  if (n0 || n1 || n2 || n3) {
-    if (n0) lo = (lo & 0xFFFF0000u) | 0x7FC0u;
-    if (n1) lo = (lo & 0x0000FFFFu) | 0x7FC00000u;
-    if (n2) hi = (hi & 0xFFFF0000u) | 0x7FC0u;
-    if (n3) hi = (hi & 0x0000FFFFu) | 0x7FC00000u;
-  }
-  return make_uint2(lo, hi);
+// alpha * sa and sb as per-tensor values (1 where absent or a vector), read with scalar loads when the
+// kernel starts so that their latency hides behind the K loop
+__device__ __forceinline__ void epilogue_scales(const Epilogue &e, float &sa1, float &sb1) {
+  typedef const __attribute__((address_space(4))) float *scalar_ptr;
+  sa1 = e.alpha * (e.sa && !e.sa_vec ? *(scalar_ptr)e.sa : 1.f);
+  sb1 = e.sb && !e.sb_vec ? *(scalar_ptr)e.sb : 1.f;
 }
 
-// The direct epilogue of a full tile with no bias and beta = 0: scale, convert and store straight from
-// the accumulators, column by column (y outer): the 16 stores into one column's cache lines follow each
-// other, so the L2 writes the lines back whole (x / g outer measured 3x the write traffic).  AMAX: fold
-// |value| for amax (compiled out otherwise: the epilogue is VALU-bound with one wave per SIMD).
-template <int DT, bool AMAX>
-__device__ __forceinline__ float direct_epilogue(const Epilogue &e, v16f (&acc)[4][4], int i0, int j0, int wm, int wn,
-                                                 int lane) {
+// ---- epilogues of full tiles: staged through the LDS ring ----------------------------------------
+// Straight from the accumulators each lane holds 4 consecutive rows of one column per block and group,
+// so a store instruction would write 8-16 bytes into each of 32 columns.  Staging the tile in the ring
+// (free once the K loop's last fragments are read) lets every store instruction write whole columns:
+// 8 full 128-byte lines.  Measured on the 8192^3 headline (one block per CU): 21.7K cycles of epilogue
+// per tile with the direct stores, 12.6K staged.
+//
+// Lane layout of an accumulator block (x, y) of wave (wm, wn): lane l, register 4 g + q holds output
+//   i = 128 wm + 32 x + 8 g + 4 (l / 32) + q,  j = 128 wn + 32 y + l % 32   (tile coordinates).
+
+// Every NaN among the pairs' BF16 codes becomes 0x7FC0 (include/e5m2effma.h; reference rne_hi)
+__device__ __forceinline__ uint32_t bf16_pair_canonical(uint32_t w) {
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const uint32_t v = (w >> (16 * h)) & 0xFFFFu;
+    if ((v & 0x7FFFu) > 0x7F80u) w = (w & ~(0xFFFFu << (16 * h))) | (0x7FC0u << (16 * h));
+  }
+  return w;
+}
+
+// Set by any lane of the block whose converted values include a NaN (staged16)
+__shared__ int g_nan_flag;
+
+// Full tile, 2-byte output (BF16 / FP16), no bias, beta = 0.  sa1 = alpha * sa, sb1 = sb (per-tensor
+// values, read before the K loop); row / column scale vectors and amax are wave-uniform run-time choices.
+// Phase W: v = acc * ((alpha * sa[i]) * sb[j]) converted to DT; lanes l and l + 32 hold rows 8g..8g+3 and
+// 8g+4..8g+7 of one column, and one v_permlane32_swap per dword (which exchanges lanes 32..63 of its
+// first operand with lanes 0..31 of its second) pairs groups 2p and 2p + 1 so that lane l holds rows
+// 16p..16p+7 and lane l + 32 rows 16p+8..16p+15: 16 bytes each, written to column j of the ring (512 bytes;
+// 32 columns per 16 KiB buffer) at 16-byte chunk k ^ (j % 16), so that the 16 lanes a ds_*_b128 serves per
+// cycle meet 16 distinct bank groups.  BF16 uses the hardware pair conversion, which keeps a NaN's sign and
+// payload: every lane folds 0 * v into a screen that is NaN exactly when some value is NaN or Inf, and a
+// block-wide flag then makes phase R rewrite NaN codes (rare path).
+// Phase R: step q writes tile columns 8q .. 8q + 7, thread t column 8q + t / 32, rows 8 (t % 32) .. + 7.
+template <int DT>
+__device__ __forceinline__ float staged16(const Epilogue &e, v16f (&acc)[4][4], int i0, int j0, int wm, int wn,
+                                          int lane, int tid, float sa1, float sb1) {
+  static_assert(elem_bytes(DT) == 2, "2-byte outputs");
   float mx = 0.f;
-  const EpiState st = epi_begin(e);
-  const int ib0 = i0 + 128 * wm + 4 * (lane >> 5);
-  const float sa1 = e.alpha * scale_or_one(e.sa), sb1 = scale_or_one(e.sb);
+  const float s = sa1 * sb1;
+  const bool vs = e.sa_vec || e.sb_vec, amax = e.amax != nullptr;  // wave-uniform
+  const int lc = lane & 31, hi = lane >> 5;
+  float screen[2] = {0.f, 0.f};
+  if (tid == 0) g_nan_flag = 0;
+  __syncthreads();  // every wave has read its last fragments from the ring
 #pragma unroll
   for (int y = 0; y < 4; ++y) {
-    const int j = j0 + 128 * wn + 32 * y + (lane & 31);
-    const float sbj = e.sb_vec ? e.sb[j] : sb1;
-    uint8_t *colp = (uint8_t *)e.d + ((size_t)j * e.ldd + ib0) * elem_bytes(DT);
+    const float sbj = e.sb_vec ? e.sb[j0 + 128 * wn + 32 * y + lc] : sb1;
+    uint8_t *col = (uint8_t *)stage_at(4 * wn + y) + lc * 512;
 #pragma unroll
     for (int x = 0; x < 4; ++x)
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
+      for (int p = 0; p < 2; ++p) {
         __builtin_amdgcn_sched_barrier(0);
-        const int ib = ib0 + 32 * x + 8 * g;
-        float as[4];  // alpha * sa[i] of these 4 rows (OUTER scaling of A)
-        if (e.sa_vec) {
-          const float4 v = *(const float4 *)(e.sa + ib);
-          as[0] = e.alpha * v.x; as[1] = e.alpha * v.y; as[2] = e.alpha * v.z; as[3] = e.alpha * v.w;
-        } else {
-          as[0] = as[1] = as[2] = as[3] = sa1;
-        }
-        float v[4];
+        uint32_t w[4];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const float sc = (e.sa_vec || e.sb_vec) ? as[q] * sbj : st.s;
-          v[q] = acc_read(acc[x][y][4 * g + q]) * sc;
-          if constexpr (AMAX) mx = amax_fold(mx, v[q]);
+        for (int h = 0; h < 2; ++h) {
+          const int g = 2 * p + h;
+          float v[4];
+          if (vs) {
+            float as[4];
+            if (e.sa_vec) {
+              const float4 a4 = *(const float4 *)(e.sa + i0 + 128 * wm + 32 * x + 8 * g + 4 * hi);
+              as[0] = e.alpha * a4.x; as[1] = e.alpha * a4.y; as[2] = e.alpha * a4.z; as[3] = e.alpha * a4.w;
+            } else {
+              as[0] = as[1] = as[2] = as[3] = sa1;
+            }
+#pragma unroll
+            for (int q = 0; q < 4; ++q) v[q] = acc_read(acc[x][y][4 * g + q]) * (as[q] * sbj);
+          } else {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) v[q] = acc_read(acc[x][y][4 * g + q]) * s;
+          }
+          if constexpr (DT == E5MA_BF16) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) screen[q & 1] = __builtin_fmaf(0.f, v[q], screen[q & 1]);
+          }
+          if (amax) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) mx = amax_fold(mx, v[q]);
+          }
+          if constexpr (DT == E5MA_BF16) {
+            typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+            w[2 * h] = __builtin_bit_cast(uint32_t, bf16x2_t{(__bf16)v[0], (__bf16)v[1]});
+            w[2 * h + 1] = __builtin_bit_cast(uint32_t, bf16x2_t{(__bf16)v[2], (__bf16)v[3]});
+          } else {
+            w[2 * h] = encode_t<DT>(v[0], 1.f) | encode_t<DT>(v[1], 1.f) << 16;
+            w[2 * h + 1] = encode_t<DT>(v[2], 1.f) | encode_t<DT>(v[3], 1.f) << 16;
+          }
         }
-        uint8_t *dp = colp + (32 * x + 8 * g) * elem_bytes(DT);
+        // (w0, w1): rows 8(2p) + 4 hi .. + 3; (w2, w3): rows 8(2p + 1) + 4 hi .. + 3
+        const auto s0 = __builtin_amdgcn_permlane32_swap(w[0], w[2], false, false);
+        const auto s1 = __builtin_amdgcn_permlane32_swap(w[1], w[3], false, false);
+        const int chunk = 16 * wm + 4 * x + 2 * p + hi;
+        *(uint4 *)(col + ((chunk ^ (lc & 15)) << 4)) = make_uint4(s0[0], s1[0], s0[1], s1[1]);
+      }
+  }
+  if constexpr (DT == E5MA_BF16) {
+    if (__builtin_isnan(screen[0] + screen[1])) g_nan_flag = 1;
+  }
+  __syncthreads();
+  const bool fix = DT == E5MA_BF16 && g_nan_flag != 0;
+  const int cq = tid >> 5, k = tid & 31;
+  uint8_t *gp = (uint8_t *)e.d + ((size_t)(j0 + cq) * e.ldd + i0 + 8 * k) * 2;
+  const size_t gstep = (size_t)16 * e.ldd;  // 8 columns
+#pragma unroll
+  for (int q = 0; q < 32; ++q) {
+    const int cl = 8 * (q & 3) + cq;  // column within ring buffer q / 4
+    uint4 d = *(const uint4 *)((const uint8_t *)stage_at(q >> 2) + cl * 512 + ((k ^ (cl & 15)) << 4));
+    if (fix) {
+      d.x = bf16_pair_canonical(d.x); d.y = bf16_pair_canonical(d.y);
+      d.z = bf16_pair_canonical(d.z); d.w = bf16_pair_canonical(d.w);
+    }
+    *(uint4 *)(gp + q * gstep) = d;
+  }
+  return mx;
+}
+
+// Full tile, any output dtype, bias and beta * C (CT: C's dtype, -1 when beta = 0), 4-element aligned
+// D and C: two passes, one per half of the tile's columns (128 columns x 256 rows of FP32,
+// the whole ring).
+// Phase W: the two waves holding the half write v = acc * ((alpha * sa[i]) * sb[j]), 4 rows (16 bytes) per
+// lane and group, column c of the half at 1 KiB in buffer c / 16, 16-byte chunk k at k ^ (c % 16).
+// Phase R: thread t takes rows 4 (t % 64) .. + 3 of column 4q + t / 64 of the half (q = 0..31), so C is
+// read and D written along whole columns; v = v + bias[i]; v = fma(beta, C * csinv, v); amax; convert
+// (the order of include/e5m2effma.h).  C may alias D: every element is read before the same thread
+// writes it.
+template <int DT, int CT>
+__device__ __forceinline__ float staged_general(const Epilogue &e, v16f (&acc)[4][4], int i0, int j0, int wm,
+                                                int wn, int lane, int tid, float sa1, float sb1) {
+  float mx = 0.f;
+  const float s = sa1 * sb1;
+  const bool vs = e.sa_vec || e.sb_vec;
+  const int lc = lane & 15, hi = lane >> 5, kr = tid & 63, cq = tid >> 6;
+  const int i = i0 + 4 * kr;  // phase R rows i .. i + 3
+  float rb[4] = {0.f, 0.f, 0.f, 0.f};
+  if (e.bias) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) rb[r] = load_any(e.bias_dtype, e.bias, (size_t)(i + r), 1.f);
+  }
+  const float csinv = scale_or_one(e.c_sinv), qs = scale_or_one(e.d_scale);
+  const bool amax = e.amax != nullptr;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    __syncthreads();  // the ring is free: the K loop's fragments, or the previous half, have been read
+    if (wn == h) {
+#pragma unroll
+      for (int y = 0; y < 4; ++y) {
+        const int c = 32 * y + (lane & 31);  // column within the half
+        float sbj = sb1;
+        if (e.sb_vec) sbj = e.sb[j0 + 128 * h + c];
+        // buffer c / 16 = 2 y + (lane & 16 ? 1 : 0): a select between two pointers, not a lane-indexed switch
+        float *colp = ((lane & 16) ? stage_at(2 * y + 1) : stage_at(2 * y)) + lc * 256;
+#pragma unroll
+        for (int x = 0; x < 4; ++x)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            __builtin_amdgcn_sched_barrier(0);
+            const int chunk = 32 * wm + 8 * x + 2 * g + hi;  // rows 4 chunk .. + 3
+            float v[4];
+            if (vs) {
+              float as[4];
+              if (e.sa_vec) {
+                const float4 a4 = *(const float4 *)(e.sa + i0 + 4 * chunk);
+                as[0] = e.alpha * a4.x; as[1] = e.alpha * a4.y; as[2] = e.alpha * a4.z; as[3] = e.alpha * a4.w;
+              } else {
+                as[0] = as[1] = as[2] = as[3] = sa1;
+              }
+#pragma unroll
+              for (int q = 0; q < 4; ++q) v[q] = acc_read(acc[x][y][4 * g + q]) * (as[q] * sbj);
+            } else {
+#pragma unroll
+              for (int q = 0; q < 4; ++q) v[q] = acc_read(acc[x][y][4 * g + q]) * s;
+            }
+            *(float4 *)(colp + ((chunk ^ lc) << 2)) = make_float4(v[0], v[1], v[2], v[3]);
+          }
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < 32; ++q) {
+      // loads of at most 8 steps in flight (32 + 32 VGPRs): unbounded, the compiler hoists all 32 and spills
+      if (q % 8 == 0) __builtin_amdgcn_sched_barrier(0);
+      const int cl = 4 * (q & 3) + cq;  // column within ring buffer q / 4
+      const int j = j0 + 128 * h + 4 * q + cq;
+      const float4 x4 = *(const float4 *)(stage_at(q >> 2) + cl * 256 + ((kr ^ cl) << 2));
+      float v[4] = {x4.x, x4.y, x4.z, x4.w};
+      float cv[4] = {0.f, 0.f, 0.f, 0.f};
+      if constexpr (CT == kAnyC) {
+        if (e.beta != 0.f) {  // beta = 0: there is no C (NULL), and none is read
+#pragma unroll
+          for (int r = 0; r < 4; ++r) cv[r] = load_any(e.c_dtype, e.c, (size_t)j * e.ldc + i + r, csinv);
+        }
+      } else if constexpr (CT >= 0) {
+        load4_t<CT>(e.c, (size_t)j * e.ldc + i, csinv, cv);  // C 4-element aligned (class precondition)
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        if (e.bias) v[r] = v[r] + rb[r];
+        if constexpr (CT == kAnyC) {
+          if (e.beta != 0.f) v[r] = __builtin_fmaf(e.beta, cv[r], v[r]);
+        } else if constexpr (CT != -1) {
+          v[r] = __builtin_fmaf(e.beta, cv[r], v[r]);
+        }
+      }
+      if (amax) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) mx = amax_fold(mx, v[r]);
+        asm volatile("" : "+v"(mx));  // folded here: sunk to the end, it keeps every value alive (spills)
+      }
+      if constexpr (DT == kAnyD) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) store_any(e.d_dtype, e.d, (size_t)j * e.ldd + i + r, v[r], qs);
+      } else {
+        uint8_t *dp = (uint8_t *)e.d + ((size_t)j * e.ldd + i) * elem_bytes(DT);
         if constexpr (DT == E5MA_FP32) {
           *(float4 *)dp = make_float4(v[0], v[1], v[2], v[3]);
         } else if constexpr (is_fp8(DT)) {
-          *(uint32_t *)dp = encode_t<DT>(v[0], st.qscale) | encode_t<DT>(v[1], st.qscale) << 8 |
-                            encode_t<DT>(v[2], st.qscale) << 16 | encode_t<DT>(v[3], st.qscale) << 24;
-        } else if constexpr (DT == E5MA_BF16) {
-          *(uint2 *)dp = bf16_quad(v);
+          *(uint32_t *)dp = encode_t<DT>(v[0], qs) | encode_t<DT>(v[1], qs) << 8 | encode_t<DT>(v[2], qs) << 16 |
+                            encode_t<DT>(v[3], qs) << 24;
         } else {
           *(uint2 *)dp = make_uint2(encode_t<DT>(v[0], 1.f) | encode_t<DT>(v[1], 1.f) << 16,
                                     encode_t<DT>(v[2], 1.f) | encode_t<DT>(v[3], 1.f) << 16);
         }
       }
+    }
   }
   return mx;
 }
 
-// The direct epilogue of a full tile with a bias and / or beta * C (C of dtype CT, -1 when beta = 0, with
-// 4-element aligned columns): the direct epilogue's layout and column order, with C read in that same
-// layout, 16 bytes (FP32) per lane and (x, g).  Units u = 4 y + x (4 loads each, g = 0..3) stream
-// through a ring of kSlots units, refilled as each unit is consumed: 24 loads per lane in flight
-// (96 VGPRs), where staging through LDS, 8 columns per thread per step, kept a third of that in flight.
-// The bias of the tile's 256 rows goes to LDS once (FP32).  Same operation order as general_half:
-// v = acc * ((alpha * sa[i]) * sb[j]); v + bias[i]; fma(beta, C, v).  C may alias D: each element is
-// loaded before the same thread stores it.  All threads of the block must call it (two barriers).
-template <int DT, int CT>
-__device__ __forceinline__ float direct_general(const Epilogue &e, v16f (&acc)[4][4], int i0, int j0, int wm, int wn,
-                                                int lane, int tid) {
-  constexpr int kSlots = 6;
+// Tiles at the m / n edges (or unaligned D): half a tile at a time -- the 128 columns of the waves with
+// wn == h, 256 x 128 FP32 = the whole ring, column group c (16 columns) in ring buffer c -- is staged in
+// LDS, then the block writes it out with bounds checks (general_half, dtypes at run time).
+__device__ __forceinline__ float edge_epilogue(const TileArgs &t, const Epilogue &e, v16f (&acc)[4][4], int i0, int j0,
+                                               int wm, int wn, int lane, int tid, int vec) {
   float mx = 0.f;
   const EpiState st = epi_begin(e);
-  const int ib0 = i0 + 128 * wm + 4 * (lane >> 5);
-  const float sa1 = e.alpha * scale_or_one(e.sa), sb1 = scale_or_one(e.sb);
-  float *bias_lds = stage_at(0);
-  __syncthreads();  // the ring is no longer read
-  bias_lds[tid] = e.bias ? load_any(e.bias_dtype, e.bias, (size_t)(i0 + tid), 1.f) : 0.f;
-  __syncthreads();
-  float cv[kSlots][4][4];
-  const auto load_unit = [&](int u, float (&c)[4][4]) {
-    const int y = u >> 2, x = u & 3;
-    const size_t at = (size_t)(j0 + 128 * wn + 32 * y + (lane & 31)) * e.ldc + ib0 + 32 * x;
+  const int i = i0 + 4 * (tid & 63);  // this thread's 4 rows in the write-out
+  float rs[4], rb[4];                 // alpha * sa[i], bias[i] of those rows
 #pragma unroll
-    for (int g = 0; g < 4; ++g) load4_t<CT>(e.c, at + 8 * g, st.csinv, c[g]);
-  };
-  if constexpr (CT >= 0) {
-#pragma unroll
-    for (int u = 0; u < kSlots; ++u) load_unit(u, cv[u]);
+  for (int q = 0; q < 4; ++q) {
+    const int iq = min(i + q, t.m - 1);
+    rs[q] = e.alpha * (e.sa_vec ? e.sa[iq] : scale_or_one(e.sa));
+    rb[q] = e.bias ? load_any(e.bias_dtype, e.bias, (size_t)iq, 1.f) : 0.f;
   }
 #pragma unroll
-  for (int u = 0; u < 16; ++u) {
-    const int y = u >> 2, x = u & 3;
-    const int j = j0 + 128 * wn + 32 * y + (lane & 31);
-    const float sbj = e.sb_vec ? e.sb[j] : sb1;
-    uint8_t *colp = (uint8_t *)e.d + ((size_t)j * e.ldd + ib0 + 32 * x) * elem_bytes(DT);
+  for (int h = 0; h < 2; ++h) {
+    __syncthreads();  // the ring (K loop) or the previous half is no longer read
+    if (wn == h) {
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      __builtin_amdgcn_sched_barrier(0);
-      const int il = 128 * wm + 32 * x + 8 * g + 4 * (lane >> 5);
-      const float4 b4 = *(const float4 *)(bias_lds + il);
-      const float rb[4] = {b4.x, b4.y, b4.z, b4.w};
-      float as[4];
-      if (e.sa_vec) {
-        const float4 v = *(const float4 *)(e.sa + i0 + il);
-        as[0] = e.alpha * v.x; as[1] = e.alpha * v.y; as[2] = e.alpha * v.z; as[3] = e.alpha * v.w;
-      } else {
-        as[0] = as[1] = as[2] = as[3] = sa1;
-      }
-      float v[4];
+      for (int y = 0; y < 4; ++y) {
+        float *grp = (lane & 16) ? stage_at(2 * y + 1) : stage_at(2 * y);
+        float *col = grp + (lane & 15) * kBM;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const float sc = (e.sa_vec || e.sb_vec) ? as[q] * sbj : st.s;
-        v[q] = acc_read(acc[x][y][4 * g + q]) * sc;
-        if (e.bias) v[q] = v[q] + rb[q];
-        if constexpr (CT >= 0) v[q] = __builtin_fmaf(e.beta, cv[u % kSlots][g][q], v[q]);
-        mx = amax_fold(mx, v[q]);
-      }
-      uint8_t *dp = colp + 8 * g * elem_bytes(DT);
-      if constexpr (DT == E5MA_FP32) {
-        *(float4 *)dp = make_float4(v[0], v[1], v[2], v[3]);
-      } else if constexpr (is_fp8(DT)) {
-        *(uint32_t *)dp = encode_t<DT>(v[0], st.qscale) | encode_t<DT>(v[1], st.qscale) << 8 |
-                          encode_t<DT>(v[2], st.qscale) << 16 | encode_t<DT>(v[3], st.qscale) << 24;
-      } else if constexpr (DT == E5MA_BF16) {
-        *(uint2 *)dp = bf16_quad(v);
-      } else {
-        *(uint2 *)dp = make_uint2(encode_t<DT>(v[0], 1.f) | encode_t<DT>(v[1], 1.f) << 16,
-                                  encode_t<DT>(v[2], 1.f) | encode_t<DT>(v[3], 1.f) << 16);
+        for (int x = 0; x < 4; ++x)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const int il = 128 * wm + 32 * x + 8 * g + 4 * (lane >> 5);
+            *(float4 *)(col + il) = make_float4(acc_read(acc[x][y][4 * g]), acc_read(acc[x][y][4 * g + 1]),
+                                                acc_read(acc[x][y][4 * g + 2]), acc_read(acc[x][y][4 * g + 3]));
+          }
       }
     }
-    // unit u's slot is free: refill it with unit u + kSlots
-    if constexpr (CT >= 0) {
-      __builtin_amdgcn_sched_barrier(0);
-      if (u + kSlots < 16) load_unit(u + kSlots, cv[u % kSlots]);
-    }
+    __syncthreads();
+    mx = general_half<kAnyD, kAnyC>(e, st, t, i, j0 + 128 * h, rs, rb, vec, tid, mx);
   }
   return mx;
 }
 
-// The epilogue of a block tile (acc: this wave's accumulators; i0, j0: the tile's origin).  Returns the
-// thread's max |value| for amax.
-template <int DT>
-__device__ __forceinline__ float tile_epilogue(const TileArgs &t, const Epilogue &e, v16f (&acc)[4][4], int i0, int j0,
-                                               int wm, int wn, int lane, int tid, int simple, int vec) {
-  // ---- epilogue.  Lane l, register r of block (x, y): output
-  //   i = i0 + 128*wm + 32*x + 8*(r/4) + 4*(l/32) + r%4,  j = j0 + 128*wn + 32*y + l%32
-  // (scheduling barriers keep the compiler from hoisting epilogue work into the K loop's tail and from
-  // copying all accumulators to VGPRs at once, both of which spill)
-  __builtin_amdgcn_sched_barrier(0);
-  float mx = 0.f;
-  if (simple && i0 + kBM <= t.m && j0 + kBN <= t.n) {
-    // no bias, beta = 0, a full tile, D aligned for 4-element stores
-    mx = e.amax ? direct_epilogue<DT, true>(e, acc, i0, j0, wm, wn, lane)
-                : direct_epilogue<DT, false>(e, acc, i0, j0, wm, wn, lane);
-  } else if (vec && i0 + kBM <= t.m && j0 + kBN <= t.n &&
-             (e.beta == 0.f ||
-              (e.c_dtype == E5MA_FP32 && (uintptr_t)e.c % 16 == 0 && e.ldc % 4 == 0))) {
-    // a full tile with a bias and / or beta * FP32 C (TE's wgrad into main_grad), D and C aligned
-    mx = e.beta != 0.f ? direct_general<DT, E5MA_FP32>(e, acc, i0, j0, wm, wn, lane, tid)
-                       : direct_general<DT, -1>(e, acc, i0, j0, wm, wn, lane, tid);
-  } else {
-    // general epilogue (bias, beta * C, tails): half a tile at a time -- the 128 columns of the waves
-    // with wn == h, 256 x 128 FP32 = the whole ring, column group c (16 columns) in ring buffer c --
-    // is staged in LDS, then the block writes it out (general_half)
-    const EpiState st = epi_begin(e);
-    const int i = i0 + 4 * (tid & 63);  // this thread's 4 rows in the write-out
-    float rs[4], rb[4];                 // alpha * sa[i], bias[i] of those rows
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int iq = min(i + q, t.m - 1);
-      rs[q] = e.alpha * (e.sa_vec ? e.sa[iq] : scale_or_one(e.sa));
-      rb[q] = e.bias ? load_any(e.bias_dtype, e.bias, (size_t)iq, 1.f) : 0.f;
-    }
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      __syncthreads();  // the ring (K loop) or the previous half is no longer read
-      if (wn == h) {
-#pragma unroll
-        for (int y = 0; y < 4; ++y) {
-          float *grp = (lane & 16) ? stage_at(2 * y + 1) : stage_at(2 * y);
-          float *col = grp + (lane & 15) * kBM;
-#pragma unroll
-          for (int x = 0; x < 4; ++x)
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-              const int il = 128 * wm + 32 * x + 8 * g + 4 * (lane >> 5);
-              *(float4 *)(col + il) = make_float4(acc_read(acc[x][y][4 * g]), acc_read(acc[x][y][4 * g + 1]),
-                                                  acc_read(acc[x][y][4 * g + 2]), acc_read(acc[x][y][4 * g + 3]));
-            }
-        }
-      }
-      __syncthreads();
-      const int c = e.beta != 0.f ? e.c_dtype : -1;
-      if (c == E5MA_FP32) mx = general_half<DT, E5MA_FP32>(e, st, t, i, j0 + 128 * h, rs, rb, vec, tid, mx);
-      else if (c == E5MA_BF16) mx = general_half<DT, E5MA_BF16>(e, st, t, i, j0 + 128 * h, rs, rb, vec, tid, mx);
-      else if (c == E5MA_FP16) mx = general_half<DT, E5MA_FP16>(e, st, t, i, j0 + 128 * h, rs, rb, vec, tid, mx);
-      else if (c == E5MA_E5M2) mx = general_half<DT, E5MA_E5M2>(e, st, t, i, j0 + 128 * h, rs, rb, vec, tid, mx);
-      else if (c == E5MA_E4M3) mx = general_half<DT, E5MA_E4M3>(e, st, t, i, j0 + 128 * h, rs, rb, vec, tid, mx);
-      else mx = general_half<DT, -1>(e, st, t, i, j0 + 128 * h, rs, rb, vec, tid, mx);
-    }
+
+// Epilogue classes, one kernel instance each (kernels holding every epilogue spill registers, and the
+// spills cost the headline GEMM 4.6%): kEpiFast16 -- every tile full, no bias, beta = 0, a 2-byte D with
+// 16-byte aligned columns (staged16); kEpiFull -- every tile full, 4-element aligned D (staged_general);
+// kEpiAny -- everything, edge tiles included.
+constexpr int kEpiFast16 = 0, kEpiFull = 1, kEpiAny = 2;
+
+// the class a launch takes (host side)
+inline int epilogue_class(int m, int n, const Epilogue &e, int simple, int vec) {
+  const bool all_full = m % kBM == 0 && n % kBN == 0;
+  const bool two_byte = e.d_dtype == E5MA_BF16 || e.d_dtype == E5MA_FP16;
+  if (all_full && simple && two_byte && (uintptr_t)e.d % 16 == 0 && e.ldd % 8 == 0) return kEpiFast16;
+  const bool c_ok = e.beta == 0.f || ((uintptr_t)e.c % (4 * elem_bytes(e.c_dtype)) == 0 && e.ldc % 4 == 0);
+  return all_full && vec && c_ok ? kEpiFull : kEpiAny;
+}
+
+// staged_general for D / C dtypes chosen at run time (the common pairings have their own instances)
+__device__ __forceinline__ float staged_full(const Epilogue &e, v16f (&acc)[4][4], int i0, int j0, int wm, int wn,
+                                             int lane, int tid, float sa1, float sb1) {
+  const int dt = e.d_dtype, c = e.beta != 0.f ? e.c_dtype : -1;
+  if (dt == E5MA_FP32 && c == E5MA_FP32)
+    return staged_general<E5MA_FP32, E5MA_FP32>(e, acc, i0, j0, wm, wn, lane, tid, sa1, sb1);
+  if (c == -1) {
+    if (dt == E5MA_FP32) return staged_general<E5MA_FP32, -1>(e, acc, i0, j0, wm, wn, lane, tid, sa1, sb1);
+    if (dt == E5MA_BF16) return staged_general<E5MA_BF16, -1>(e, acc, i0, j0, wm, wn, lane, tid, sa1, sb1);
+    if (dt == E5MA_E5M2) return staged_general<E5MA_E5M2, -1>(e, acc, i0, j0, wm, wn, lane, tid, sa1, sb1);
+    if (dt == E5MA_E4M3) return staged_general<E5MA_E4M3, -1>(e, acc, i0, j0, wm, wn, lane, tid, sa1, sb1);
   }
-  return mx;
+  return staged_general<kAnyD, kAnyC>(e, acc, i0, j0, wm, wn, lane, tid, sa1, sb1);
+}
+
+// The epilogue of a block tile (acc: this wave's accumulators; i0, j0: the tile's origin; sa1 = alpha * sa
+// and sb1 = sb, the per-tensor scales read before the K loop) for D of any dtype (e.d_dtype), in class
+// EPI.  Returns the thread's max |value| for amax.
+template <int EPI>
+__device__ __forceinline__ float tile_epilogue(const TileArgs &t, const Epilogue &e, v16f (&acc)[4][4], int i0, int j0,
+                                               int wm, int wn, int lane, int tid, int simple, int vec, float sa1,
+                                               float sb1) {
+  // (a scheduling barrier keeps the compiler from hoisting epilogue work into the K loop's tail)
+  __builtin_amdgcn_sched_barrier(0);
+  if constexpr (EPI == kEpiFast16) {
+    return e.d_dtype == E5MA_BF16 ? staged16<E5MA_BF16>(e, acc, i0, j0, wm, wn, lane, tid, sa1, sb1)
+                                  : staged16<E5MA_FP16>(e, acc, i0, j0, wm, wn, lane, tid, sa1, sb1);
+  } else if constexpr (EPI == kEpiFull) {
+    return staged_full(e, acc, i0, j0, wm, wn, lane, tid, sa1, sb1);
+  } else {
+    const bool full = i0 + kBM <= t.m && j0 + kBN <= t.n;
+    if (full && simple && (e.d_dtype == E5MA_BF16 || e.d_dtype == E5MA_FP16) && ((uintptr_t)e.d & 15) == 0 &&
+        (e.ldd & 7) == 0)
+      return e.d_dtype == E5MA_BF16 ? staged16<E5MA_BF16>(e, acc, i0, j0, wm, wn, lane, tid, sa1, sb1)
+                                    : staged16<E5MA_FP16>(e, acc, i0, j0, wm, wn, lane, tid, sa1, sb1);
+    const bool c_ok = e.beta == 0.f || ((uintptr_t)e.c % (4 * elem_bytes(e.c_dtype)) == 0 && e.ldc % 4 == 0);
+    if (full && vec && c_ok) return staged_full(e, acc, i0, j0, wm, wn, lane, tid, sa1, sb1);
+    return edge_epilogue(t, e, acc, i0, j0, wm, wn, lane, tid, vec);
+  }
 }
 
 }  // namespace tile
