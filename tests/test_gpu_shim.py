@@ -1,278 +1,260 @@
-"""The Python layer (matmul / linear / cast / adam_step / AdamW / Float8Tensor / quantize_linear_) on the
-GPU.  Results are held to a float64 product with the bound
-|y - ref| <= half an output ulp * |ref| + k * 2^-23 * sum|a*b| (the contract's FP32 accumulation error),
-codecs are compared with torch's own conversions, and the optimizer with torch.optim.AdamW.  Mirrors the
-coverage of the reference's binds/python/tests/test_e5m2effma.py:42-336."""
+"""The torch layer (e5m2effma_amd: matmul, linear, cast, adam_step, AdamW, Float8Tensor, quantize_linear_)
+on the GPU, checked against the CPU oracle: GEMM results against the accumulation bound, casts, Adam steps
+and quantization bit for bit.  Row-major products are checked as the column-major GEMM the layer issues
+(out^T = b^T a^T, reference binds/python/csrc/e5m2effma_torch.cpp:179-197)."""
+import numpy as np
 import pytest
 import torch
-import torch.nn.functional as Fn
+import torch.nn.functional as F
 
 import e5m2effma_amd as fx
+import gpu_util as gu
+import oracle
 
 pytestmark = pytest.mark.gpu
-DEV = "cuda"
-F8, F4 = torch.float8_e5m2, torch.float8_e4m3fn
-TOP = {F8: 57344.0, F4: 448.0}
-HALF_ULP = {torch.bfloat16: 2.0 ** -8, torch.float16: 2.0 ** -11, torch.float32: 2.0 ** -24, F8: 2.0 ** -3,
-            F4: 2.0 ** -4}
+DEV = torch.device("cuda:0")
+CODE = {torch.float8_e5m2: oracle.E5M2, torch.float8_e4m3fn: oracle.E4M3, torch.bfloat16: oracle.BF16,
+        torch.float16: oracle.FP16, torch.float32: oracle.FP32}
+NPV = {torch.float8_e5m2: np.uint8, torch.float8_e4m3fn: np.uint8, torch.bfloat16: np.uint16,
+       torch.float16: np.uint16, torch.float32: np.float32}
+RAW = {np.uint8: torch.uint8, np.uint16: torch.int16, np.float32: torch.float32}
 
 
-def rand(shape, dtype, scale=1.0, seed=0):
-    g = torch.Generator().manual_seed(seed)
-    return (torch.randn(shape, generator=g) * scale).to(DEV).to(dtype)
+def host(t):
+    """A tensor's elements as the oracle's numpy codes (row-major, contiguous)."""
+    t = t.detach().contiguous()
+    raw = t.view(RAW[NPV[t.dtype]]) if t.dtype != torch.float32 else t
+    return raw.cpu().numpy().view(NPV[t.dtype]).ravel().copy()
 
 
-def within_bound(y, ref, mag, k, out_dtype):
-    err = (y.double() - ref).abs()
-    bound = HALF_ULP[out_dtype] * ref.abs() + k * 2.0 ** -23 * mag + 1e-30
-    excess = (err - bound * 1.0001).max()
-    assert float(excess) <= 0, f"bound exceeded by {float(excess)}"
+def device(codes, dtype, shape):
+    t = torch.from_numpy(np.ascontiguousarray(codes).view(np.uint8 if NPV[dtype] == np.uint8 else NPV[dtype]))
+    if dtype == torch.float32:
+        return t.reshape(shape).to(DEV)
+    return t.view(RAW[NPV[dtype]]).reshape(shape).to(DEV).view(dtype)
 
 
-def product(a, b, sa=1.0, sb=1.0, bias=None):
-    A, B = a.double() * sa, b.double() * sb
-    r = A @ B
-    if bias is not None:
-        r = r + bias.double()
-    return r, A.abs() @ B.abs()
+def operand(rng, dtype, shape, sigma=2.0):
+    n = int(np.prod(shape))
+    if dtype in (torch.float8_e5m2, torch.float8_e4m3fn):
+        return device(gu.normal_fp8(rng, n, CODE[dtype], sigma), dtype, shape)
+    x = (rng.standard_normal(n) * sigma).astype(np.float32)
+    return device(x if dtype == torch.float32 else oracle.encode(CODE[dtype], x), dtype, shape)
 
 
-OPS = [F8, F4, torch.bfloat16, torch.float32]
+def check_product(a, b, out, *, alpha=1.0, beta=0.0, out0=None, bias=None, scale_a=None, scale_b=None,
+                  scale_out=None, amax=None):
+    """out (row-major [M, N]) against the oracle bound for alpha * (sa * sb) * (a @ b) + bias + beta * out0."""
+    M, K = a.shape
+    N = b.shape[1]
+    sa = None if scale_a is None else host(scale_a.float())
+    sb = None if scale_b is None else host(scale_b.float())
+    D0 = host(out0) if out0 is not None else np.zeros(M * N, NPV[out.dtype])
+    g = oracle.Gemm(1, 0, N, M, K, alpha, CODE[b.dtype], host(b.t()), K, CODE[a.dtype], host(a), K,
+                    sa=sb, sa_vec=sb is not None and sb.size > 1, sb=sa, sb_vec=sa is not None and sa.size > 1,
+                    beta=beta, ddt=CODE[out.dtype], D=D0.copy(), ldd=N,
+                    qscale=1.0 if scale_out is None else float(scale_out.item()),
+                    biasdt=CODE[bias.dtype] if bias is not None else oracle.FP32,
+                    bias=None if bias is None else host(bias), ocp_operands=True)
+    iis, jjs = [v.ravel() for v in np.meshgrid(np.arange(N), np.arange(M), indexing="ij")]
+    bad, first, alo, ahi = g.check(host(out), D0 if beta != 0.0 else None, iis, jjs)
+    assert bad == 0, (bad, first)
+    if amax is not None:
+        got = float(amax.item())
+        assert alo <= got <= ahi or got == alo == ahi, (got, alo, ahi)
 
 
-@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
-@pytest.mark.parametrize("b_layout", ["row", "col"])
-@pytest.mark.parametrize("tb", OPS)
-@pytest.mark.parametrize("ta", OPS)
-def test_matmul(ta, tb, b_layout, out_dtype):
-    M, K, N = 70, 96, 50
-    a = rand((M, K), ta, seed=1)
-    b = rand((K, N), tb, seed=2) if b_layout == "row" else rand((N, K), tb, seed=2).t()
-    y = fx.matmul(a, b, out_dtype=out_dtype)
-    assert y.shape == (M, N) and y.dtype == out_dtype
-    within_bound(y, *product(a, b), K, out_dtype)
+@pytest.mark.parametrize("adt,bdt,odt", [(torch.float8_e5m2, torch.float8_e4m3fn, torch.bfloat16),
+                                         (torch.float8_e4m3fn, torch.float8_e5m2, torch.float32),
+                                         (torch.float8_e5m2, torch.bfloat16, torch.float16),
+                                         (torch.bfloat16, torch.float8_e4m3fn, torch.bfloat16)])
+@pytest.mark.parametrize("b_t", [False, True])
+def test_matmul_pairings_and_b_layouts(adt, bdt, odt, b_t):
+    rng = np.random.default_rng(100 * CODE[adt] + 10 * CODE[bdt] + int(b_t))
+    M, K, N = 72, 96, 40
+    a = operand(rng, adt, (M, K))
+    b = operand(rng, bdt, (N, K)).t() if b_t else operand(rng, bdt, (K, N))
+    sa = torch.tensor([0.75], device=DEV) if adt in (torch.float8_e5m2, torch.float8_e4m3fn) else None
+    sb = torch.tensor([1.5], device=DEV) if bdt in (torch.float8_e5m2, torch.float8_e4m3fn) else None
+    out = fx.matmul(a, b, out_dtype=odt, scale_a=sa, scale_b=sb, alpha=0.5)
+    assert out.shape == (M, N) and out.dtype == odt
+    check_product(a, b, out, alpha=0.5, scale_a=sa, scale_b=sb)
 
 
-@pytest.mark.parametrize("tw", [F8, F4])
-@pytest.mark.parametrize("tx", OPS)
-@pytest.mark.parametrize("rows", [1, 3, 8, 9, 64])
-def test_linear_fp8_weight(rows, tx, tw):  # rows <= 8: the GEMV kernel
-    N, K = 300, 512
-    w, x = rand((N, K), tw, seed=3), rand((rows, K), tx, seed=4)
-    bias = rand((N,), torch.bfloat16, seed=5)
-    y = fx.linear(x, w, bias, scale_w=torch.tensor([0.25], device=DEV))
-    within_bound(y, *product(x, w.t(), sb=0.25, bias=bias), K, torch.bfloat16)
-
-
-def test_linear_batched_shape():
-    assert fx.linear(rand((2, 3, 64), torch.bfloat16), rand((40, 64), F8, seed=1)).shape == (2, 3, 40)
-
-
-def test_accumulate_into_fp32_out():
-    M, K, N = 33, 64, 47
-    a, b = rand((M, K), torch.bfloat16, seed=1), rand((K, N), torch.bfloat16, seed=2)
-    out = rand((M, N), torch.float32, seed=3)
-    start = out.clone()
-    fx.matmul(a, b, out=out, beta=1.0)
-    ref, mag = product(a, b)
-    within_bound(out, ref + start.double(), mag + start.double().abs(), K, torch.float32)
-
-
-@pytest.mark.parametrize("out", [F8, F4])
-def test_fp8_output_scale_amax(out):
-    M, K, N = 16, 64, 32
-    a, b = rand((M, K), F8, seed=1), rand((K, N), F4, seed=2)
-    scale, amax = torch.tensor([4.0], device=DEV), torch.zeros(1, device=DEV)
-    y = fx.matmul(a, b, out_dtype=out, scale_out=scale, amax_out=amax)
-    ref, _ = product(a, b)
-    assert y.dtype == out
-    assert float(amax) == pytest.approx(float(ref.abs().max()), rel=2 ** -20)
-    expect = (ref * 4.0).clamp(-TOP[out], TOP[out]).float().to(out)
-    assert torch.equal(y.view(torch.uint8), expect.view(torch.uint8))
-
-
-@pytest.mark.parametrize("dtype", [F8, F4, torch.bfloat16, torch.float16])
-def test_cast_matches_torch(dtype):
-    x = rand((1000, 37), torch.float32, scale=50.0).clamp(-448, 448)
-    assert torch.equal(fx.cast(x, dtype).view(torch.uint8), x.to(dtype).view(torch.uint8))
-
-
-@pytest.mark.parametrize("dtype", [F8, F4])
-def test_cast_scale_roundtrip(dtype):
-    x = rand((4096,), torch.float32)
-    amax, scale = torch.zeros(1, device=DEV), torch.tensor([64.0], device=DEV)
-    q = fx.cast(x, dtype, scale=scale, amax=amax)
-    assert float(amax) == float(x.abs().max())
-    back = fx.cast(q, torch.float32, scale_inv=torch.tensor([1 / 64.0], device=DEV))
-    assert torch.equal(back, (x * 64).to(dtype).float() / 64)
-
-
-def test_cast_e5m2_inf_nan_and_kat():
-    codes = torch.arange(256, device=DEV, dtype=torch.uint8).view(F8)
-    y = fx.cast(codes, torch.float32)
-    assert torch.equal(y.isinf(), codes.float().isinf()) and torch.equal(y.isnan(), codes.float().isnan())
-    amax = torch.zeros(1, device=DEV)
-    q = fx.cast(torch.tensor([1.0, float("inf"), -1e6, 3.0], device=DEV), F8, amax=amax)
-    assert q.view(torch.uint8).tolist() == [0x3C, 0x7B, 0xFB, 0x42] and float(amax) == float("inf")
-
-
-@pytest.mark.parametrize("state_dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("pdtype", [torch.float32, torch.bfloat16])
-def test_adamw_against_torch(pdtype, state_dtype):
-    torch.manual_seed(0)
-    ref = torch.nn.Parameter(torch.randn(1000, device=DEV))
-    mine = torch.nn.Parameter(ref.detach().clone().to(pdtype))
-    opt_ref = torch.optim.AdamW([ref], lr=1e-2, weight_decay=0.1, foreach=False)
-    opt = fx.AdamW([mine], lr=1e-2, weight_decay=0.1, state_dtype=state_dtype)
-    for _ in range(5):
-        g = torch.randn(1000, device=DEV)
-        ref.grad, mine.grad = g.clone(), g.to(pdtype)
-        opt_ref.step()
-        opt.step()
-    tol = 1e-6 if pdtype == torch.float32 and state_dtype == torch.float32 else 2e-2
-    torch.testing.assert_close(mine.detach().float(), ref.detach(), rtol=tol, atol=tol)
-    assert opt.state[mine]["exp_avg"].dtype == state_dtype and opt.state[mine]["step"] == 5
-
-
-@pytest.mark.parametrize("qt", [F8, F4])
-def test_adam_step_fp8_copy(qt):
-    p = rand((256,), torch.float32)
-    g, m, v = rand((256,), torch.bfloat16, seed=1), torch.zeros(256, device=DEV), torch.zeros(256, device=DEV)
-    q, amax = torch.empty(256, device=DEV, dtype=qt), torch.zeros(1, device=DEV)
-    fx.adam_step(p, g, m, v, lr=1e-3, step=1, param_fp8=q, fp8_scale=torch.tensor([8.0], device=DEV), fp8_amax=amax)
-    assert torch.equal(q.view(torch.uint8), (p * 8).to(qt).view(torch.uint8))
-    assert float(amax) == float(p.abs().max())
+def test_matmul_bias_accumulate_and_fp8_output():
+    rng = np.random.default_rng(5)
+    M, K, N = 64, 128, 48
+    a, b = operand(rng, torch.float8_e4m3fn, (M, K)), operand(rng, torch.float8_e5m2, (K, N))
+    bias = operand(rng, torch.bfloat16, (N,))
+    acc = operand(rng, torch.float32, (M, N), sigma=4.0)
+    acc0 = acc.clone()
+    fx.matmul(a, b, out=acc, beta=1.0, bias=bias)
+    check_product(a, b, acc, beta=1.0, out0=acc0, bias=bias)
+    so, am = torch.tensor([0.125], device=DEV), torch.zeros(1, device=DEV)
+    o8 = fx.matmul(a, b, out_dtype=torch.float8_e5m2, scale_out=so, amax_out=am)
+    check_product(a, b, o8, scale_out=so, amax=am)
 
 
 @pytest.mark.parametrize("which", ["a", "b", "both"])
-def test_matmul_rowwise_scales(which):
-    M, K, N = 70, 96, 50
-    a, b = rand((M, K), F8, seed=1), rand((N, K), F4, seed=2).t()
-    sa = torch.rand(M, device=DEV) + 0.5 if which in ("a", "both") else torch.tensor([0.75], device=DEV)
-    sb = torch.rand(N, device=DEV) + 0.5 if which in ("b", "both") else torch.tensor([1.5], device=DEV)
-    for out_dtype in (torch.bfloat16, torch.float32):
-        y = fx.matmul(a, b, scale_a=sa, scale_b=sb, out_dtype=out_dtype)
-        sa2 = sa.double().reshape(-1, 1) if sa.numel() > 1 else sa.double()
-        sb2 = sb.double().reshape(1, -1) if sb.numel() > 1 else sb.double()
-        within_bound(y, *product(a, b, sa2, sb2), K, out_dtype)
+def test_matmul_row_and_column_scales(which):
+    rng = np.random.default_rng(len(which))
+    M, K, N = 80, 64, 56
+    a, b = operand(rng, torch.float8_e5m2, (M, K)), operand(rng, torch.float8_e4m3fn, (K, N))
+    sa = torch.from_numpy(rng.uniform(0.25, 2, M).astype(np.float32)).to(DEV) if which != "b" else None
+    sb = torch.from_numpy(rng.uniform(0.25, 2, N).astype(np.float32)).to(DEV) if which != "a" else None
+    out = fx.matmul(a, b, scale_a=sa, scale_b=sb)
+    check_product(a, b, out, scale_a=sa, scale_b=sb)
 
 
-@pytest.mark.parametrize("rows", [1, 8, 64])
-def test_linear_per_channel_weight_scale(rows):
-    N, K = 300, 512
-    w, x = rand((N, K), F8, seed=3), rand((rows, K), torch.bfloat16, seed=4)
-    sw = torch.rand(N, device=DEV) + 0.5
-    y = fx.linear(x, w, scale_w=sw)
-    within_bound(y, *product(x, w.t(), sb=sw.double().reshape(1, -1)), K, torch.bfloat16)
+@pytest.mark.parametrize("rows", [1, 5, 8, 33])
+def test_linear_with_per_channel_weight_scale(rows):
+    """rows <= 8 run the GEMV kernel (x row-major, W FP8 K-contiguous), more rows the tiled GEMM."""
+    rng = np.random.default_rng(rows)
+    K, Nout = 256, 96
+    x = operand(rng, torch.bfloat16, (rows, K), sigma=1.0)
+    w = operand(rng, torch.float8_e4m3fn, (Nout, K))
+    sw = torch.from_numpy(rng.uniform(0.01, 0.05, Nout).astype(np.float32)).to(DEV)
+    bias = operand(rng, torch.float32, (Nout,))
+    y = fx.linear(x, w, bias, scale_w=sw)
+    assert y.shape == (rows, Nout)
+    check_product(x, w.t(), y, bias=bias, scale_b=sw)
 
 
-# ---- Float8Tensor ---------------------------------------------------------------------------------
-@pytest.mark.parametrize("rows", [1, 8, 64])
-@pytest.mark.parametrize("per_row", [False, True])
-@pytest.mark.parametrize("fp8", [F8, F4])
-def test_float8tensor_linear(fp8, per_row, rows):
-    w, x = rand((300, 512), torch.bfloat16, seed=3), rand((rows, 512), torch.bfloat16, seed=4)
-    w8 = fx.Float8Tensor.from_float(w, fp8=fp8, per_row=per_row)
-    assert isinstance(w8, fx.Float8Tensor) and w8.dtype == torch.bfloat16 and w8.shape == w.shape
-    assert w8._data.dtype == fp8
-    bias = rand((300,), torch.bfloat16, seed=5)
-    y = Fn.linear(x, w8, bias)
-    assert y.dtype == torch.bfloat16 and not isinstance(y, fx.Float8Tensor)
-    s = w8._scale_inv if per_row else w8._scale_inv.reshape(())
-    assert torch.equal(y, fx.linear(x, w8._data, scale_w=s, bias=bias))  # the same kernel call
-    assert torch.equal(x @ w8.t() + 0, fx.linear(x, w8._data, scale_w=s))
-    wd = w8.dequantize(torch.float64)
-    within_bound(y, x.double() @ wd.t() + bias.double(), x.double().abs() @ wd.abs().t(), 512, torch.bfloat16)
+def test_linear_keeps_leading_dims():
+    rng = np.random.default_rng(9)
+    x = operand(rng, torch.bfloat16, (2, 3, 64))
+    w = operand(rng, torch.float8_e5m2, (32, 64))
+    y = fx.linear(x, w)
+    assert y.shape == (2, 3, 32)
+    check_product(x.reshape(6, 64), w.t(), y.reshape(6, 32))
 
 
-def test_float8tensor_both_operands():
-    a8 = fx.Float8Tensor.from_float(rand((70, 96), torch.float32, seed=1), per_row=True, dtype=torch.float32)
-    b8 = fx.Float8Tensor.from_float(rand((50, 96), torch.float32, seed=2), per_row=True, dtype=torch.float32)
-    y = a8 @ b8.t()  # per-row scales of both operands are outer: one FP8 x FP8 GEMM
+def test_large_product_splits_k_with_a_torch_workspace():
+    """A 4-tile output at k = 8192 runs e5ma_gemm_ex with a split-K workspace from torch's allocator."""
+    rng = np.random.default_rng(11)
+    M = N = 512
+    K = 8192
+    a, b = operand(rng, torch.float8_e5m2, (M, K), 4.0), operand(rng, torch.float8_e4m3fn, (K, N), 4.0)
+    # row-major a, b issue e5ma_gemm_ex(N, N, N, M, K) with A := b (lda N), B := a (ldb K)
+    assert fx._lib.workspace_size(0, 0, N, M, K, oracle.E4M3, N, oracle.E5M2, K) > 0
+    out = fx.matmul(a, b, out_dtype=torch.float32)
+    check_product(a, b, out)
+
+
+@pytest.mark.parametrize("src,dst", [(torch.float32, torch.float8_e5m2), (torch.bfloat16, torch.float8_e4m3fn),
+                                     (torch.float8_e5m2, torch.float32), (torch.float8_e4m3fn, torch.bfloat16)])
+def test_cast_is_the_oracle_cast(src, dst):
+    rng = np.random.default_rng(3)
+    x = operand(rng, src, (1000, 3), sigma=300.0)
+    si = torch.tensor([0.5], device=DEV) if src in (torch.float8_e5m2, torch.float8_e4m3fn) else None
+    sc = torch.tensor([0.25], device=DEV) if dst in (torch.float8_e5m2, torch.float8_e4m3fn) else None
+    am = torch.zeros(1, device=DEV)
+    y = fx.cast(x, dst, scale_inv=si, scale=sc, amax=am)
+    want, want_amax = oracle.cast(CODE[src], CODE[dst], host(x), x.numel(), 1.0 if si is None else 0.5,
+                                  1.0 if sc is None else 0.25)
+    assert np.array_equal(host(y), want) and np.float32(am.item()) == np.float32(want_amax)
+
+
+@pytest.mark.parametrize("pdt,sdt", [(torch.float32, torch.float32), (torch.bfloat16, torch.bfloat16),
+                                     (torch.float32, torch.bfloat16)])
+def test_adamw_optimizer_matches_the_oracle(pdt, sdt):
+    """Three steps of fx.AdamW over two parameters (one with a grad scale group option), bit for bit
+    against the oracle's element order."""
+    rng = np.random.default_rng(17)
+    shapes = [(33, 17), (1000,)]
+    params = [torch.nn.Parameter(operand(rng, pdt, s, 0.5)) for s in shapes]
+    opt = fx.AdamW(params, lr=1e-3, weight_decay=0.05, state_dtype=sdt, grad_scale=0.5)
+    ref = [dict(p=host(p), m=np.zeros(p.numel(), NPV[sdt]), v=np.zeros(p.numel(), NPV[sdt])) for p in params]
+    for step in range(1, 4):
+        for p, r in zip(params, ref):
+            g = operand(rng, pdt, p.shape, 1e-2)  # torch ties .grad's dtype to the parameter's
+            p.grad = g
+            r["g"] = host(g)
+        opt.step()
+        cfg = dict(lr=1e-3, beta1=0.9, beta2=0.999, eps=1e-8, weight_decay=0.05, step=step, adamw=1,
+                   bias_correction=1, grad_scale=0.5)
+        for p, r in zip(params, ref):
+            oracle.adam(cfg, CODE[pdt], r["p"], CODE[pdt], r["g"], CODE[sdt], r["m"], r["v"], threads=4)
+            st = opt.state[p]
+            assert st["step"] == step
+            assert np.array_equal(host(p.data), r["p"]), f"param after step {step}"
+            assert np.array_equal(host(st["exp_avg"]), r["m"]) and np.array_equal(host(st["exp_avg_sq"]), r["v"])
+
+
+def test_adamw_fp8_copy_with_delayed_scaling():
+    """fp8_copy: each step's copy is the updated weights quantized with the previous step's amax."""
+    rng = np.random.default_rng(23)
+    p = torch.nn.Parameter(operand(rng, torch.float32, (4096,), 0.02))
+    opt = fx.AdamW([p], lr=1e-3, fp8_copy=torch.float8_e4m3fn)
+    amax_prev = float(p.detach().abs().max())
+    for step in range(1, 4):
+        p.grad = operand(rng, torch.float32, (4096,), 1e-3)
+        opt.step()
+        st = opt.state[p]
+        scale = np.float32(st["fp8_scale"].item())  # torch's 448 / amax: reciprocal() * 448 on the device
+        assert scale == pytest.approx(448.0 / max(amax_prev, 1e-12), rel=2e-7)
+        w = host(p.data)
+        assert np.array_equal(host(st["param_fp8"]), oracle.encode(oracle.E4M3, w, float(scale)))
+        amax_prev = float(np.abs(w).max())
+        assert np.float32(st["fp8_amax"].item()) == np.float32(amax_prev)
+        assert float(st["fp8_scale_inv"].item()) == pytest.approx(1.0 / float(scale), rel=2e-7)
+
+
+@pytest.mark.parametrize("fp8,per_row", [(torch.float8_e4m3fn, True), (torch.float8_e5m2, False)])
+def test_float8tensor_from_float_and_products(fp8, per_row):
+    rng = np.random.default_rng(int(per_row) + 7)
+    w = torch.from_numpy((rng.standard_normal((96, 128)) * 0.05).astype(np.float32)).to(DEV)
+    q = fx.Float8Tensor.from_float(w, fp8=fp8, per_row=per_row, dtype=torch.bfloat16)
+    codes, sinv, _ = oracle.quantize(oracle.FP32, CODE[fp8], host(w), 96, 128,
+                                     57344.0 if fp8 == torch.float8_e5m2 else 448.0, per_row=per_row)
+    assert np.array_equal(host(q.codes), codes) and np.array_equal(host(q.scale_inv), sinv)
+    x = operand(rng, torch.bfloat16, (40, 128), 1.0)
+    bias = operand(rng, torch.bfloat16, (96,), 1.0)
+    for y in (F.linear(x, q, bias), torch.addmm(bias, x, q.t()), x @ q.t() + 0 * bias):
+        assert type(y) is torch.Tensor and y.dtype == torch.bfloat16 and y.shape == (40, 96)
+    y = F.linear(x, q, bias)
+    check_product(x, q.codes.t(), y, bias=bias, scale_b=q.scale_inv)
+    y2 = torch.addmm(bias, x, q.t(), alpha=0.5)
+    check_product(x, q.codes.t(), y2, alpha=0.5, bias=bias, scale_b=q.scale_inv)
+
+
+def test_float8tensor_both_operands_fp8():
+    rng = np.random.default_rng(29)
+    a32 = torch.from_numpy((rng.standard_normal((64, 96)) * 3).astype(np.float32)).to(DEV)
+    b32 = torch.from_numpy((rng.standard_normal((80, 96)) * 0.1).astype(np.float32)).to(DEV)
+    qa = fx.Float8Tensor.from_float(a32, fp8=torch.float8_e5m2, per_row=True, dtype=torch.float32)
+    qb = fx.Float8Tensor.from_float(b32, fp8=torch.float8_e4m3fn, per_row=True, dtype=torch.float32)
+    y = qa @ qb.t()
     assert y.dtype == torch.float32
-    assert torch.equal(y, fx.matmul(a8._data, b8._data.t(), scale_a=a8._scale_inv, scale_b=b8._scale_inv,
-                                    out_dtype=torch.float32))
-    ad, bd = a8.dequantize(torch.float64), b8.dequantize(torch.float64)
-    within_bound(y, ad @ bd.t(), ad.abs() @ bd.abs().t(), 96, torch.float32)
-    # a scale along K (a8 as the right operand without transpose) can only be applied by dequantizing
-    z = b8.t().t() @ a8.t()
-    assert torch.allclose(z, b8.float() @ a8.float().t(), rtol=1e-5, atol=1e-4)
-    w = a8.t() @ a8  # both scales run along K: dequantized product
-    assert torch.allclose(w, a8.float().t() @ a8.float(), rtol=1e-5, atol=1e-4)
+    check_product(qa.codes, qb.codes.t(), y, scale_a=qa.scale_inv, scale_b=qb.scale_inv)
 
 
 def test_quantize_linear_module():
+    rng = np.random.default_rng(31)
     torch.manual_seed(0)
-    m = torch.nn.Sequential(torch.nn.Linear(512, 256), torch.nn.GELU(), torch.nn.Linear(256, 64),
-                            torch.nn.Linear(64, 8, bias=False), torch.nn.Linear(8, 8)).to(DEV, torch.bfloat16)
-    x = rand((4, 7, 512), torch.bfloat16, seed=6)
-    with torch.no_grad():
-        ref = m(x).float()
-        fx.quantize_linear_(m)
-        y = m(x).float()
-    assert [isinstance(l.weight, fx.Float8Tensor) for l in m if isinstance(l, torch.nn.Linear)] == \
-        [True, True, True, False]  # in_features 8 is not a multiple of 16: kept
-    assert float((y - ref).norm() / ref.norm()) < 0.1
+    model = torch.nn.Sequential(torch.nn.Linear(64, 48), torch.nn.ReLU(), torch.nn.Linear(48, 24),
+                                torch.nn.Linear(24, 8)).to(DEV).to(torch.bfloat16)
+    fx.quantize_linear_(model)
+    l0, l2, l3 = model[0], model[2], model[3]
+    assert isinstance(l0.weight, fx.Float8Tensor) and isinstance(l2.weight, fx.Float8Tensor)
+    assert not isinstance(l3.weight, fx.Float8Tensor)  # in_features 24 is not a multiple of 16
+    assert l0.weight.codes.dtype == torch.float8_e4m3fn and l0.weight.scale_dim == 0
+    x = operand(rng, torch.bfloat16, (16, 64), 1.0)
+    h = model[0](x)
+    check_product(x, l0.weight.codes.t(), h, bias=l0.bias, scale_b=l0.weight.scale_inv)
+    assert model(x).shape == (16, 8)
 
 
-def test_float8tensor_from_float_per_row_needs_2d():
-    with pytest.raises(ValueError, match="per_row"):
-        fx.Float8Tensor.from_float(torch.ones(2, 3, 16, device=DEV), per_row=True)
-
-
-# ---- rejection of bad input -----------------------------------------------------------------------
-def test_rejects_bad_dtype_and_shapes():
-    with pytest.raises(TypeError):
-        fx.matmul(torch.zeros(16, 16, device=DEV, dtype=torch.float64), rand((16, 16), F8))
-    with pytest.raises(TypeError):
-        fx.matmul(rand((16, 16), torch.float16), rand((16, 16), F8))
-    with pytest.raises(ValueError, match="shapes"):
-        fx.matmul(rand((8, 32), F8), rand((16, 8), F8))
-    with pytest.raises(ValueError, match="shape"):
-        fx.linear(rand((4, 32), torch.bfloat16), rand((8, 48), F8))
-    with pytest.raises(ValueError, match="multiple of 16"):
-        fx.matmul(rand((8, 24), F8), rand((24, 8), F8))
-
-
-@pytest.mark.parametrize("view", ["offset", "strided", "row_major_n_not_16"])
-def test_awkward_layouts_are_repacked(view):
-    base = rand((40, 130), F8, seed=7)
-    a = {"offset": base[:, 1:129], "strided": base[:, ::2][:, :64], "row_major_n_not_16": base[:, :128]}[view]
-    b = rand((a.shape[1], 50), torch.bfloat16, seed=8)
-    y = fx.matmul(a, b)
-    assert torch.equal(y, fx.matmul(a.contiguous(), b.t().contiguous().t()))
-    within_bound(y, *product(a, b), a.shape[1], torch.bfloat16)
-
-
-def test_rejects_misused_scales_and_out():
-    with pytest.raises(ValueError, match="scale_a"):
-        fx.matmul(rand((8, 16), torch.bfloat16), rand((16, 8), F8), scale_a=torch.ones(1, device=DEV))
-    with pytest.raises(TypeError, match="float32"):
-        fx.matmul(rand((8, 16), F8), rand((16, 8), F8), scale_a=torch.ones(1, device=DEV, dtype=torch.float64))
-    with pytest.raises(ValueError, match="one element"):
-        fx.matmul(rand((8, 16), F8), rand((16, 8), F8), scale_a=torch.ones(2, device=DEV))
-    a, b = rand((8, 16), F8), rand((16, 8), F8)
-    with pytest.raises(ValueError, match="out must be given"):
-        fx.matmul(a, b, beta=1.0)
-    with pytest.raises(ValueError, match="shape"):
-        fx.matmul(a, b, out=torch.empty(8, 9, device=DEV, dtype=torch.bfloat16))
-    with pytest.raises(ValueError, match="row-contiguous"):
-        fx.matmul(a, b, out=torch.empty(8, 8, device=DEV, dtype=torch.bfloat16).t())
-    x = rand((16, 16), torch.float32)
-    with pytest.raises(ValueError, match="share memory"):
-        fx.matmul(x, rand((16, 16), torch.float32, seed=1), out=x)
-
-
-def test_rejects_adam_problems():
-    p, g = rand((10,), torch.float32), rand((10,), torch.float32)
-    m, v = torch.zeros(10, device=DEV), torch.zeros(10, device=DEV)
-    with pytest.raises(ValueError, match="step"):
-        fx.adam_step(p, g, m, v, lr=1e-3, step=0)
-    with pytest.raises(ValueError, match="elements"):
-        fx.adam_step(p, g[:5], m, v, lr=1e-3, step=1)
-    with pytest.raises(TypeError, match="exp_avg_sq"):
-        fx.adam_step(p, g, m, v.bfloat16(), lr=1e-3, step=1)
-    with pytest.raises(ValueError, match="share memory"):
-        fx.adam_step(p, g, m, m, lr=1e-3, step=1)
-    with pytest.raises(ValueError, match="betas"):
-        fx.adam_step(p, g, m, v, lr=1e-3, betas=(0.9, 1.0), step=1)
+@pytest.mark.parametrize("call,exc,text", [
+    (lambda: fx.matmul(torch.zeros(16, 16, device=DEV, dtype=torch.float16), torch.zeros(16, 16, device=DEV)),
+     TypeError, "float16"),
+    (lambda: fx.matmul(torch.zeros(16, 24, device=DEV), torch.zeros(24, 16, device=DEV)), ValueError, "multiple of 16"),
+    (lambda: fx.matmul(torch.zeros(16, 16, device=DEV), torch.zeros(32, 16, device=DEV)), ValueError, "shapes"),
+    (lambda: fx.matmul(torch.zeros(16, 16, device=DEV), torch.zeros(16, 16, device=DEV), beta=1.0),
+     ValueError, "out must be given"),
+    (lambda: fx.adam_step(*(torch.zeros(4, device=DEV) for _ in range(4)), lr=1e-3, step=0), ValueError, "step"),
+    (lambda: fx.cast(torch.zeros(4, device=DEV), torch.int8), TypeError, "dtype"),
+])
+def test_errors_map_to_python_exceptions(call, exc, text):
+    with pytest.raises(exc, match=text):
+        call()
