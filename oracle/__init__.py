@@ -75,6 +75,7 @@ def lib():
                 "orc_lane_batch": (None, [vp, vp, vp, i, i, vp, sz]),
                 "orc_lane_compare": (sz, [vp, vp, sz, i, i, vp]),
                 "orc_lane_sweep": (None, [vp, vp, sz, i, i, vp]),
+                "orc_lane_gemm": (None, [vp, vp, vp, i, i, i, i, vp, i, i]),
                 "orc_encode_selfcheck": (sz, [i, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_uint64, vp]),
                 "orc_cast": (f, [i, i, vp, vp, sz, f, f, f]),
                 "orc_quantize": (None, [i, i, vp, vp, sz, sz, f, f, i, vp, vp]),
@@ -140,6 +141,28 @@ def lane_sweep(accs, fa, fb, fn=None):
     ptr = None if fn is None else ctypes.cast(fn, ctypes.c_void_p)
     lib().orc_lane_sweep(ptr, _p(accs), accs.size, fa, fb, _p(out))
     return out
+
+
+def lane_gemm(a, b, M, N, K, fa, fb, fn=None, rows=None, threads=1):
+    """BASELINE config 1's CPU path: row-major a (M x K) times b (K x N), FP8 codes of formats fa / fb
+    (1 = E5M2), as a BF16-accumulating chain of a lane function over k (default: the oracle's; fn: a
+    ctypes function pointer such as the reference's ref_lane).  Returns the BF16 bits of rows
+    rows[0] .. rows[1] - 1 (all rows by default), computed by `threads` threads."""
+    r0, r1 = (0, M) if rows is None else rows
+    a = np.ascontiguousarray(a, np.uint8)
+    b = np.ascontiguousarray(b, np.uint8)
+    out = np.zeros(M * N, np.uint16)
+    ptr = None if fn is None else ctypes.cast(fn, ctypes.c_void_p)
+    bounds = np.linspace(r0, r1, max(1, min(threads, r1 - r0)) + 1).astype(np.int64)
+
+    def work(t):
+        lib().orc_lane_gemm(ptr, _p(a), _p(b), N, K, fa, fb, _p(out), int(bounds[t]), int(bounds[t + 1]))
+    ths = [threading.Thread(target=work, args=(t,)) for t in range(len(bounds) - 1)]
+    for t in ths:
+        t.start()
+    for t in ths:
+        t.join()
+    return out.reshape(M, N)[r0:r1]
 
 
 def cast(tin, tout, src, count, sinv=1.0, qscale=1.0, amax_in=0.0):

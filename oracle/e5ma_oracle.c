@@ -259,6 +259,24 @@ void orc_lane_sweep(orc_ref_lane_fn fn, const uint16_t *accs, size_t nacc, int f
             fn ? (uint16_t)fn(a, b, accs[c], fa, fb) : orc_lane((uint8_t)a, (uint8_t)b, accs[c], fa, fb);
 }
 
+/* BASELINE config 1's CPU path: a row-major M x K by K x N product of FP8 codes as a chain of the
+ * reference's MAC model over k (tests/e5m2effma_ref.h:114-129): out[i][j] = lane(a[i][K-1], b[K-1][j],
+ * ... lane(a[i][0], b[0][j], +0)), a BF16 accumulator rounded once per MAC.  fn: the reference's own
+ * ref_lane (compiled from its sources into _ref/libref.so) or NULL for the restatement above.  Rows
+ * row0 .. row1 - 1 of out (BF16 bits). */
+void orc_lane_gemm(orc_ref_lane_fn fn, const uint8_t *a, const uint8_t *b, int N, int K, int fa, int fb,
+                   uint16_t *out, int row0, int row1) {
+  for (int i = row0; i < row1; ++i)
+    for (int j = 0; j < N; ++j) {
+      uint16_t acc = 0;
+      for (int k = 0; k < K; ++k) {
+        const uint8_t x = a[(size_t)i * K + k], y = b[(size_t)k * N + j];
+        acc = fn ? (uint16_t)fn(x, y, acc, fa, fb) : orc_lane(x, y, acc, fa, fb);
+      }
+      out[(size_t)i * N + j] = acc;
+    }
+}
+
 /* ---------------------------------------------------------------------------------------------
  * e5ma_cast (src/e5m2effma.cu:53-63, 85-101): v = load(src) * sinv; amax = max |v|;
  * dst = store(v, qscale).  Returns the updated amax.

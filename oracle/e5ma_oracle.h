@@ -43,6 +43,8 @@ void orc_lane_batch(const uint8_t *a, const uint8_t *b, const uint16_t *acc, int
 typedef uint32_t (*orc_ref_lane_fn)(uint32_t, uint32_t, uint32_t, int, int);
 size_t orc_lane_compare(orc_ref_lane_fn ref, const uint16_t *accs, size_t nacc, int fa, int fb,
                         uint32_t *first_bad);
+void orc_lane_gemm(orc_ref_lane_fn fn, const uint8_t *a, const uint8_t *b, int N, int K, int fa, int fb,
+                   uint16_t *out, int row0, int row1);
 void orc_lane_sweep(orc_ref_lane_fn fn, const uint16_t *accs, size_t nacc, int fa, int fb,
                     uint16_t *out);
 size_t orc_encode_selfcheck(int fmt, uint64_t start, uint64_t stop, uint64_t step, uint32_t *first_bad);

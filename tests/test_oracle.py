@@ -452,3 +452,116 @@ def test_adam_fp8_copy_and_amax(orc):
     ref = orc.encode(0, pf, 64.0)
     assert (np.abs(orc.decode(0, q).astype(np.float64) - orc.decode(0, ref)) <=
             np.abs(orc.decode(0, ref)) * 2.0 ** -3 + 2.0 ** -9).all()
+
+
+# ---- Adam's operation order, bit for bit -------------------------------------------------------------
+def _rn32(x):
+    """Round a Fraction to the nearest float32 (ties to even), exactly; overflow to +-inf."""
+    from fractions import Fraction
+    if x == 0:
+        return np.float32(0.0)
+    sign, x = (-1 if x < 0 else 1), abs(Fraction(x))
+    e = x.numerator.bit_length() - x.denominator.bit_length()
+    if Fraction(2) ** e > x:
+        e -= 1
+    e = max(e, -126)                  # below 2^-126 the grid is the subnormal one, spacing 2^-149
+    q = x / Fraction(2) ** (e - 23)   # the significand on a 24-bit integer grid
+    n, r = divmod(q.numerator, q.denominator)
+    if 2 * r > q.denominator or (2 * r == q.denominator and n % 2 == 1):
+        n += 1
+    v = float(n) * 2.0 ** (e - 23)
+    return np.float32(sign * v) if abs(v) < 2.0 ** 128 else np.float32(sign * np.inf)
+
+
+def _adam_exact_model(cfg, p, g, m, v):
+    """One step of include/e5m2effma.h's documented order on float32 values, each operation rounded once
+    from its exact value (an FMA: one rounding of a * b + c).  Coefficients as the host forms them: in
+    double, rounded to float32 once (reference src/adamw_e5m2effma.cu:150-157)."""
+    from fractions import Fraction as Fr
+    import math
+    f = lambda x: Fr(float(x))
+    c1, c2 = np.float32(1.0 - float(np.float32(cfg["beta1"]))), np.float32(1.0 - float(np.float32(cfg["beta2"])))
+    b1, b2 = np.float32(cfg["beta1"]), np.float32(cfg["beta2"])
+    corr = lambda b: np.float32(1.0 / (1.0 - float(b) ** cfg["step"])) if cfg["bias_correction"] else np.float32(1)
+    r1, r2 = corr(b1), corr(b2)
+    lr, wd, eps = np.float32(cfg["lr"]), np.float32(cfg["weight_decay"]), np.float32(cfg["eps"])
+    decay = np.float32(float(lr) * float(wd))
+    gs = np.float32(cfg["grad_scale"] or 1.0)
+    out = []
+    for pi, gi, mi, vi in zip(p, g, m, v):
+        gg = _rn32(f(gi) * f(gs))
+        if not cfg["adamw"]:
+            gg = _rn32(f(wd) * f(pi) + f(gg))
+        mm = _rn32(f(b1) * f(mi) + f(_rn32(f(c1) * f(gg))))
+        vv = _rn32(f(b2) * f(vi) + f(_rn32(f(c2) * f(_rn32(f(gg) * f(gg))))))
+        num = _rn32(f(mm) * f(r1))
+        root = np.float32(math.sqrt(float(_rn32(f(vv) * f(r2)))))  # 53 >= 2 * 24 + 2: double rounding is exact
+        u = _rn32(f(num) / f(_rn32(f(root) + f(eps))))
+        pp = pi
+        if cfg["adamw"]:
+            pp = _rn32(-f(decay) * f(pp) + f(pp))
+        pp = _rn32(-f(lr) * f(u) + f(pp))
+        out.append((pp, mm, vv))
+    return [np.array(c, np.float32) for c in zip(*out)]
+
+
+@pytest.mark.parametrize("adamw,bc", [(1, 1), (0, 1), (1, 0)])
+def test_adam_order_matches_exact_model(orc, adamw, bc):
+    """The oracle's Adam step, bit for bit, against the exact-arithmetic model of the documented order on
+    random state over several steps.  A misplaced or missing FMA (m, v, the weight decay) changes the
+    result in a sizeable fraction of these elements."""
+    rng = np.random.default_rng(40 + adamw + 2 * bc)
+    n = 1500
+    p = (rng.standard_normal(n) * 0.5).astype(np.float32)
+    m = (rng.standard_normal(n) * 1e-2).astype(np.float32)
+    v = (np.abs(rng.standard_normal(n)) * 1e-4).astype(np.float32)
+    for step in (1, 2, 7):
+        g = (rng.standard_normal(n) * 3e-2).astype(np.float32)
+        cfg = dict(lr=3e-3, beta1=0.9, beta2=0.999, eps=1e-8, weight_decay=0.05, step=step, adamw=adamw,
+                   bias_correction=bc, grad_scale=0.75)
+        want_p, want_m, want_v = _adam_exact_model(cfg, p, g, m, v)
+        orc.adam(cfg, 3, p, 3, g, 3, m, v)
+        assert np.array_equal(p.view(np.uint32), want_p.view(np.uint32)), step
+        assert np.array_equal(m.view(np.uint32), want_m.view(np.uint32)), step
+        assert np.array_equal(v.view(np.uint32), want_v.view(np.uint32)), step
+
+
+def test_adam_exact_model_detects_a_misplaced_fma(orc):
+    """Negative control: the same model with m's update as two roundings (mul, then add) disagrees with
+    the oracle on these inputs, so the comparison above can tell the orders apart."""
+    from fractions import Fraction as Fr
+    rng = np.random.default_rng(47)
+    n = 1500
+    p = (rng.standard_normal(n) * 0.5).astype(np.float32)
+    m = (rng.standard_normal(n) * 1e-2).astype(np.float32)
+    v = (np.abs(rng.standard_normal(n)) * 1e-4).astype(np.float32)
+    g = (rng.standard_normal(n) * 3e-2).astype(np.float32)
+    b1, c1 = np.float32(0.9), np.float32(1.0 - float(np.float32(0.9)))
+    fused = [_rn32(Fr(float(b1)) * Fr(float(mi)) + Fr(float(_rn32(Fr(float(c1)) * Fr(float(gi))))))
+             for mi, gi in zip(m, g)]
+    split = [np.float32(b1 * mi) + _rn32(Fr(float(c1)) * Fr(float(gi))) for mi, gi in zip(m, g)]
+    assert sum(a != b for a, b in zip(fused, split)) > n // 20
+    cfg = dict(lr=3e-3, beta1=0.9, beta2=0.999, eps=1e-8, weight_decay=0.05, step=1, adamw=1,
+               bias_correction=1, grad_scale=1.0)
+    orc.adam(cfg, 3, p, 3, g, 3, m, v)
+    assert np.array_equal(m, np.array(fused, np.float32)) and not np.array_equal(m, np.array(split, np.float32))
+
+
+# ---- BASELINE config 1's CPU path: the reference's MAC chain --------------------------------------------
+def test_lane_gemm_matches_reference_lane_and_closed_form(orc):
+    rng = np.random.default_rng(51)
+    M, N, K = 24, 20, 48
+    a = orc.encode(4, (rng.standard_normal(M * K) * 4).astype(np.float32))
+    b = orc.encode(4, (rng.standard_normal(K * N) * 4).astype(np.float32))
+    got = orc.lane_gemm(a, b, M, N, K, 1, 1, threads=3)
+    ref = orc.ref_library()
+    if ref is not None:
+        assert np.array_equal(got, orc.lane_gemm(a, b, M, N, K, 1, 1, fn=ref.ref_lane))
+    # one non-zero product per output: the chain is BF16 of that product (+0 start, one rounding)
+    a1 = np.zeros(M * K, np.uint8)
+    b1 = np.zeros(K * N, np.uint8)
+    a1[np.arange(M) * K + 5] = a[:M]
+    b1[5 * N + np.arange(N)] = b[:N]
+    one = orc.lane_gemm(a1, b1, M, N, K, 1, 1)
+    prod = np.outer(orc.decode(4, a[:M]).astype(np.float64), orc.decode(4, b[:N]).astype(np.float64))
+    assert np.array_equal(one, orc.encode(1, prod.astype(np.float32)).reshape(M, N))
