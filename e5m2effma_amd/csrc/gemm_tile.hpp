@@ -379,8 +379,9 @@ __device__ __forceinline__ float staged16(const Epilogue &e, v16f (&acc)[4][4], 
 // lane and group, column c of the half at 1 KiB in buffer c / 16, 16-byte chunk k at k ^ (c % 16).
 // Phase R: thread t takes rows 4 (t % 64) .. + 3 of column 4q + t / 64 of the half (q = 0..31), so C is
 // read and D written along whole columns; v = v + bias[i]; v = fma(beta, C * csinv, v); amax; convert
-// (the order of include/e5m2effma.h).  C may alias D: every element is read before the same thread
-// writes it.
+// (the order of include/e5m2effma.h).  C is loaded a group of 8 steps ahead of its use, the next half's
+// first group before that half is staged (a load waited on right away left the TE wgrad GEMM 17% slower).
+// C may alias D: each thread reads its own elements before it writes them, and no other thread writes them.
 template <int DT, int CT>
 __device__ __forceinline__ float staged_general(const Epilogue &e, v16f (&acc)[4][4], int i0, int j0, int wm,
                                                 int wn, int lane, int tid, float sa1, float sb1) {
@@ -396,6 +397,70 @@ __device__ __forceinline__ float staged_general(const Epilogue &e, v16f (&acc)[4
   }
   const float csinv = scale_or_one(e.c_sinv), qs = scale_or_one(e.d_scale);
   const bool amax = e.amax != nullptr;
+  // C of one group of 8 write-out steps per buffer (group g: half g / 4, steps 8 (g % 4) .. + 7), loaded one
+  // group ahead of its use so that a load's latency overlaps the previous group's stores
+  float ca[8][4], cb[8][4];
+  auto load_group = [&](int g, float (&c)[8][4]) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int q = 8 * (g & 3) + u;
+      const int j = j0 + 128 * (g >> 2) + 4 * q + cq;
+      if constexpr (CT == kAnyC) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          c[u][r] = e.beta != 0.f ? load_any(e.c_dtype, e.c, (size_t)j * e.ldc + i + r, csinv) : 0.f;
+      } else if constexpr (CT >= 0) {
+        load4_t<CT>(e.c, (size_t)j * e.ldc + i, csinv, c[u]);  // C 4-element aligned (class precondition)
+      }
+    }
+  };
+  // group g's write-out with C of the group in cur, loading group g + 1's into nxt
+  auto write_group = [&](int h, int gq, float (&cur)[8][4], float (&nxt)[8][4]) {
+    const int g = 4 * h + gq;
+    if constexpr (CT != -1) {
+      if (g < 7) load_group(g + 1, nxt);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int q = 8 * gq + u;
+      const int cl = 4 * (q & 3) + cq;  // column within ring buffer q / 4
+      const int j = j0 + 128 * h + 4 * q + cq;
+      const float4 x4 = *(const float4 *)(stage_at(q >> 2) + cl * 256 + ((kr ^ cl) << 2));
+      float v[4] = {x4.x, x4.y, x4.z, x4.w};
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        if (e.bias) v[r] = v[r] + rb[r];
+        if constexpr (CT == kAnyC) {
+          if (e.beta != 0.f) v[r] = __builtin_fmaf(e.beta, cur[u][r], v[r]);
+        } else if constexpr (CT != -1) {
+          v[r] = __builtin_fmaf(e.beta, cur[u][r], v[r]);
+        }
+      }
+      if (amax) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) mx = amax_fold(mx, v[r]);
+        asm volatile("" : "+v"(mx));  // folded here: sunk to the end, it keeps every value alive (spills)
+      }
+      if constexpr (DT == kAnyD) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) store_any(e.d_dtype, e.d, (size_t)j * e.ldd + i + r, v[r], qs);
+      } else {
+        uint8_t *dp = (uint8_t *)e.d + ((size_t)j * e.ldd + i) * elem_bytes(DT);
+        if constexpr (DT == E5MA_FP32) {
+          *(float4 *)dp = make_float4(v[0], v[1], v[2], v[3]);
+        } else if constexpr (is_fp8(DT)) {
+          *(uint32_t *)dp = encode_t<DT>(v[0], qs) | encode_t<DT>(v[1], qs) << 8 | encode_t<DT>(v[2], qs) << 16 |
+                            encode_t<DT>(v[3], qs) << 24;
+        } else {
+          *(uint2 *)dp = make_uint2(encode_t<DT>(v[0], 1.f) | encode_t<DT>(v[1], 1.f) << 16,
+                                    encode_t<DT>(v[2], 1.f) | encode_t<DT>(v[3], 1.f) << 16);
+        }
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  if constexpr (CT != -1) load_group(0, ca);
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     __syncthreads();  // the ring is free: the K loop's fragments, or the previous half, have been read
@@ -433,53 +498,10 @@ __device__ __forceinline__ float staged_general(const Epilogue &e, v16f (&acc)[4
       }
     }
     __syncthreads();
-#pragma unroll
-    for (int q = 0; q < 32; ++q) {
-      // loads of at most 8 steps in flight (32 + 32 VGPRs): unbounded, the compiler hoists all 32 and spills
-      if (q % 8 == 0) __builtin_amdgcn_sched_barrier(0);
-      const int cl = 4 * (q & 3) + cq;  // column within ring buffer q / 4
-      const int j = j0 + 128 * h + 4 * q + cq;
-      const float4 x4 = *(const float4 *)(stage_at(q >> 2) + cl * 256 + ((kr ^ cl) << 2));
-      float v[4] = {x4.x, x4.y, x4.z, x4.w};
-      float cv[4] = {0.f, 0.f, 0.f, 0.f};
-      if constexpr (CT == kAnyC) {
-        if (e.beta != 0.f) {  // beta = 0: there is no C (NULL), and none is read
-#pragma unroll
-          for (int r = 0; r < 4; ++r) cv[r] = load_any(e.c_dtype, e.c, (size_t)j * e.ldc + i + r, csinv);
-        }
-      } else if constexpr (CT >= 0) {
-        load4_t<CT>(e.c, (size_t)j * e.ldc + i, csinv, cv);  // C 4-element aligned (class precondition)
-      }
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        if (e.bias) v[r] = v[r] + rb[r];
-        if constexpr (CT == kAnyC) {
-          if (e.beta != 0.f) v[r] = __builtin_fmaf(e.beta, cv[r], v[r]);
-        } else if constexpr (CT != -1) {
-          v[r] = __builtin_fmaf(e.beta, cv[r], v[r]);
-        }
-      }
-      if (amax) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) mx = amax_fold(mx, v[r]);
-        asm volatile("" : "+v"(mx));  // folded here: sunk to the end, it keeps every value alive (spills)
-      }
-      if constexpr (DT == kAnyD) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) store_any(e.d_dtype, e.d, (size_t)j * e.ldd + i + r, v[r], qs);
-      } else {
-        uint8_t *dp = (uint8_t *)e.d + ((size_t)j * e.ldd + i) * elem_bytes(DT);
-        if constexpr (DT == E5MA_FP32) {
-          *(float4 *)dp = make_float4(v[0], v[1], v[2], v[3]);
-        } else if constexpr (is_fp8(DT)) {
-          *(uint32_t *)dp = encode_t<DT>(v[0], qs) | encode_t<DT>(v[1], qs) << 8 | encode_t<DT>(v[2], qs) << 16 |
-                            encode_t<DT>(v[3], qs) << 24;
-        } else {
-          *(uint2 *)dp = make_uint2(encode_t<DT>(v[0], 1.f) | encode_t<DT>(v[1], 1.f) << 16,
-                                    encode_t<DT>(v[2], 1.f) | encode_t<DT>(v[3], 1.f) << 16);
-        }
-      }
-    }
+    write_group(h, 0, ca, cb);
+    write_group(h, 1, cb, ca);
+    write_group(h, 2, ca, cb);
+    write_group(h, 3, cb, ca);
   }
   return mx;
 }
