@@ -6,9 +6,9 @@
 // reads 1 KiB contiguous per row and pass), decodes them with the packed FP8 -> FP32 converts, and
 // FMAs them against the matching x values of every column.  The 64 partial sums of each output are
 // combined by a butterfly over the wave; lane r*n + j then runs the epilogue of output (row r, j).
-// Every weight byte is read once from HBM.  Up to n = 4 (and for FP32 x) the products run on the
-// VALU; at n = 5 .. 8 with a BF16 or FP8 x, gemv_mfma_kernel reduces 16 rows per block on the BF16
-// matrix cores.
+// Every weight byte is read once from HBM.  At n = 1 (and for FP32 x) the products run on the VALU;
+// at n = 2 .. 8 with a BF16 or FP8 x, gemv_mfma_kernel reduces 16 rows per block on the BF16 matrix
+// cores, both operands staged through LDS.
 #include "e5ma_host.hpp"
 
 namespace e5ma {
@@ -440,26 +440,31 @@ __global__ __launch_bounds__(kXThreads) void gemv_xlds_kernel(const uint8_t *A, 
   if (e.amax) amax_commit_block(e.amax, mx, red);
 }
 
-// ---- matrix-core kernel for 5 <= n <= 8 with BF16 or FP8 x ----------------------------------------
+// ---- matrix-core kernel for 2 <= n <= 8 with BF16 or FP8 x ----------------------------------------
 // A block owns 16 rows and reduces them over all of k on v_mfma_f32_16x16x32_bf16: operand A is the 16
 // rows of weights widened exactly to BF16, operand B is x widened the same way (BF16 x as is), with
 // columns n .. 15 of the 16-column operand zero.  Lane l (row / column r = l & 15, k-group g = l >> 4)
-// reads U 16-byte chunks of its row, c = cw + 4 u + g: load u of a wave reads 64 contiguous bytes of
-// each of its 16 rows (16 lines per instruction), and a batch 64 U contiguous bytes per row; MFMA (u, h) takes k 16 c + 8 h .. + 7 for A from the lane's
-// weights and for B from column r of x at the same k.  Any assignment of k to the 32 slots of one MFMA is
-// a valid reduction order as long as A and B use the same one, and they do: a lane's k depend on g only.
+// takes chunks t = g + 4u (u < U) of each batch of 4U 16-byte chunks per row; MFMA (u, h) takes k
+// 16 t + 8 h .. + 7 for A from row r and for B from column r of x at the same k.  Any assignment of k to
+// the 32 slots of one MFMA is a valid reduction order as long as A and B use the same one, and they do.
 // Products are exact and accumulate in FP32, so the result meets the same bound as the dot kernels.
-// The W waves of a block take every W-th batch; their 16 x 16 partial results are summed in wave order
-// through LDS (deterministic), then 16 n threads run the epilogue.  x comes from L2 per wave with no
-// LDS copy, so a CU holds several blocks, and x bytes are 2 n / 16 of the weight bytes per block.
-// Replaces the dot kernels' per-weight x traffic (16 B of x from LDS per weight dword at n = 8).
-// Measured on 8192 x 8192 E5M2 x BF16 (us, dot kernel -> this one, 4 chunks, 4 waves): n = 3 15.5 -> 19.5,
-// n = 4 17.6 -> 19.6, n = 5 22.3 -> 19.9, n = 6 23.2 -> 20.0, n = 7 24.1 -> 21.0, n = 8 24.7 -> 21.7; 8 chunks
-// or 8 waves per block were no faster (8 chunks: 128 VGPRs), so n <= 4 stays on the dot kernels.
+// Both operands of a batch reach the wave through its own LDS slot, filled by direct-to-LDS loads one
+// batch ahead: the weights as whole 128-byte lines of 16 / U rows per 1 KiB load, x as whole columns of
+// the batch's k range.  Loaded straight into registers in the MFMA layout, every weight instruction read
+// 64-byte halves of 16 rows and every x instruction 16 bytes from each of up to 32 lines (8 columns
+// 16 KiB apart, 4 k-groups): about 300 line requests per batch against about 60 now, and the time was
+// flat in n.  The W waves of a block take every W-th batch; their 16 x 16 partial results are summed in
+// wave order through LDS (deterministic), then 16 n threads run the epilogue.
+// Measured on 8192 x 8192 E5M2 x BF16 (us; dot kernels / earlier register-loaded MFMA kernel -> this one,
+// U = 2, 4 waves): n = 1 11.9 -> 12.4 (so n = 1 stays on the dot kernel), n = 2 13.0 -> 12.4, n = 4
+// 16.3 -> 12.7, n = 8 21.1 -> 13.0; U = 4 14.7 and 2 waves per block 15.7 at n = 8.
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+#ifndef E5MA_GEMV_MFMA_MIN_N
+#define E5MA_GEMV_MFMA_MIN_N 2  // smallest n on this kernel
+#endif
 #ifndef E5MA_GEMV_MFMA_U
-#define E5MA_GEMV_MFMA_U 4  // 16-byte chunks per lane and batch
+#define E5MA_GEMV_MFMA_U 2  // 16-byte chunks per lane and batch
 #endif
 #ifndef E5MA_GEMV_MFMA_WAVES
 #define E5MA_GEMV_MFMA_WAVES 4
@@ -470,50 +475,115 @@ constexpr int kMWaves = E5MA_GEMV_MFMA_WAVES, kMThreads = 64 * kMWaves;
 // batches (every chunk inside the row: the wave-uniform cw + 4 U <= nch) take unclamped addresses and no
 // masks; the last, partial batch clamps its addresses and zeroes out-of-range chunks as whole 32-bit words
 // (weights and x both, so that no x value past the row end meets a weight).
-template <int AT, int BT, int U, bool FULL>
-__device__ __forceinline__ void gemv_mfma_batch(const uint8_t *arow, const uint8_t *B, long long ldb, int r, bool xlane,
-                                                int cl, int nch, f32x4 &acc) {
-  u32x4 wa[U];
+// x of one batch in LDS: for each of the 8 columns the batch's 64 U values of k (kColBytes bytes) as 16-byte
+// chunks, chunk t of column j at position t ^ (j & kSwz).  The 16 lanes that read one MFMA's B fragments
+// (columns r = 0..15 at one chunk) then meet 16 distinct bank groups (lanes r and r + 8 read the same
+// address).  Filled by direct-to-LDS loads of 1 KiB, each a whole number of columns: lane s fetches
+// the chunk its LDS position holds, so the lanes of one column read its bytes contiguously.
+template <int BT, int U> struct XSlice {
+  static constexpr int kColBytes = 64 * U * elem_bytes(BT);
+  static constexpr int kChunks = kColBytes / 16;         // 16-byte chunks per column
+  static constexpr int kSwz = kChunks - 1 < 15 ? kChunks - 1 : 15;
+  static constexpr int kBytes = 8 * kColBytes;
+  static constexpr int kLoads = kBytes / 1024;          // 1 KiB loads per slice of 8 columns
+  static constexpr int kColsPerLoad = 1024 / kColBytes;
+  static_assert(kBytes % 1024 == 0 && kChunks <= 64, "whole columns per 1 KiB load");
+  // loads that cover columns 0 .. nb - 1 (the slots of the others are never read unmasked)
+  static constexpr int loads_for(int nb) { return (nb + kColsPerLoad - 1) / kColsPerLoad; }
+};
+
+// Issues the direct-to-LDS loads of the x slice for chunks c0 .. c0 + 4U - 1 of the weight row (k = 16 c0 ..)
+// into xs; columns past n repeat column n - 1 and chunks past the row end repeat its last chunk (read
+// but never multiplied: their weights and x are masked)
+template <int BT, int U, int NB>
+__device__ __forceinline__ void xslice_issue(uint8_t *xs, const uint8_t *B, long long ldb, int n, int c0, int nch,
+                                             int lane) {
+  using X = XSlice<BT, U>;
+  constexpr int kColsPerLoad = X::kColsPerLoad;
 #pragma unroll
-  for (int u = 0; u < U; ++u)
-    wa[u] = __builtin_nontemporal_load((const u32x4 *)(arow + 16 * (FULL ? cl + 4 * u : min(cl + 4 * u, nch - 1))));
-  XChunk<BT> xc[U];
-#pragma unroll
-  for (int u = 0; u < U; ++u) {
-    if (xlane) {
-      xc[u].load(B, ldb, r, FULL ? cl + 4 * u : min(cl + 4 * u, nch - 1));
-    } else {
-#pragma unroll
-      for (int d = 0; d < XChunk<BT>::kDw; ++d) xc[u].w[d] = 0u;
-    }
+  for (int q = 0; q < X::loads_for(NB); ++q) {
+    const int j = q * kColsPerLoad + lane / X::kChunks, pos = lane % X::kChunks;
+    const int t = pos ^ (j & X::kSwz);                                   // chunk of column j this lane fetches
+    const long long kk = min(16LL * c0 + (long long)t * (16 / elem_bytes(BT)), 16LL * nch - 16 / elem_bytes(BT));
+    const uint8_t *src = B + ((long long)min(j, n - 1) * ldb + kk) * elem_bytes(BT);
+    gemv_load_lds16(src, xs + 1024 * q);
   }
+}
+
+// B fragment of MFMA (u, h) for this lane (column r, k-group g) from the x slice: x values of k
+// 16 (g + 4u) + 8h .. + 7 of column r & 7 as 4 dwords of BF16 pairs
+template <int BT, int U>
+__device__ __forceinline__ u32x4 xslice_frag(const uint8_t *xs, int r, int g, int u, int h) {
+  using X = XSlice<BT, U>;
+  const int j = r & 7;
+  if constexpr (is_fp8(BT)) {
+    const int t = g + 4 * u;  // 16-byte chunk (16 codes), half h
+    const uint2 w = *(const uint2 *)(xs + j * X::kColBytes + 16 * (t ^ (j & X::kSwz)) + 8 * h);
+    bf16x2 p0, p1, p2, p3;
+    fp8x4_to_bf16<BT>(w.x, p0, p1);
+    fp8x4_to_bf16<BT>(w.y, p2, p3);
+    return u32x4{__builtin_bit_cast(uint32_t, p0), __builtin_bit_cast(uint32_t, p1), __builtin_bit_cast(uint32_t, p2),
+                 __builtin_bit_cast(uint32_t, p3)};
+  } else {
+    const int t = 2 * (g + 4 * u) + h;  // 16-byte chunk (8 BF16 values)
+    return *(const u32x4 *)(xs + j * X::kColBytes + 16 * (t ^ (j & X::kSwz)));
+  }
+}
+
+// The weights of one batch in LDS: 16 rows of 4 U chunks of 16 bytes (the batch's 64 U bytes of k), chunk t
+// of row r at position t ^ (r & kSwz), so that the 16 lanes reading one MFMA's A fragments (rows 0..15
+// at one chunk) meet distinct bank groups.  Filled by 1 KiB direct-to-LDS loads of 16 / U rows each:
+// lane s fetches the chunk its position holds, so the lanes of one row read its bytes contiguously
+// (whole 128-byte lines).
+template <int U> struct WSlice {
+  static constexpr int kChunks = 4 * U;                 // chunks per row and batch
+  static constexpr int kSwz = kChunks - 1 < 15 ? kChunks - 1 : 15;
+  static constexpr int kBytes = 16 * 16 * kChunks;
+  static constexpr int kLoads = kBytes / 1024;
+  static constexpr int kRowsPerLoad = 64 / kChunks;
+  static_assert(kBytes % 1024 == 0 && 64 % kChunks == 0, "whole rows per 1 KiB load");
+};
+
+// Issues the weight loads of the batch at chunks c0 .. c0 + 4U - 1 of rows i0 .. i0 + 15 (rows past m
+// repeat row m - 1, chunks past the row end its last chunk: read, never multiplied)
+template <int U>
+__device__ __forceinline__ void wslice_issue(uint8_t *ws, const uint8_t *A, long long lda, int i0, int m, int c0,
+                                             int nch, int lane) {
+  using W = WSlice<U>;
+#pragma unroll
+  for (int q = 0; q < W::kLoads; ++q) {
+    const int r = q * W::kRowsPerLoad + lane / W::kChunks, pos = lane % W::kChunks;
+    const int t = pos ^ (r & W::kSwz);
+    const uint8_t *src = A + (long long)min(i0 + r, m - 1) * lda + 16LL * min(c0 + t, nch - 1);
+    gemv_load_lds16(src, ws + 1024 * q);
+  }
+}
+
+// One batch's products from the two slices: A fragment (u, h) of lane (row r, group g) is half h of
+// chunk g + 4u of row r, widened exactly to BF16; chunks past the row end (FULL false) are zeroed as
+// whole words in the weights and x both
+template <int AT, int BT, int U, bool FULL>
+__device__ __forceinline__ void gemv_mfma_compute(const uint8_t *ws, const uint8_t *xs, int r, int g, bool xlane,
+                                                  int cl, int nch, f32x4 &acc) {
+  using W = WSlice<U>;
 #pragma unroll
   for (int u = 0; u < U; ++u) {
-    const uint32_t keep = FULL || cl + 4 * u < nch ? ~0u : 0u;
-    uint32_t aw[8], bw[8];
+    const uint32_t keep = FULL || cl + 4 * u < nch ? ~0u : 0u, xkeep = xlane ? keep : 0u;
+    const int t = g + 4 * u;
+    const u32x4 wa = *(const u32x4 *)(ws + r * (16 * W::kChunks) + 16 * (t ^ (r & W::kSwz)));
+    uint32_t aw[8];
 #pragma unroll
     for (int d = 0; d < 4; ++d) {
       bf16x2 lo, hi;
-      fp8x4_to_bf16<AT>(wa[u][d] & keep, lo, hi);
+      fp8x4_to_bf16<AT>(wa[d] & keep, lo, hi);
       aw[2 * d] = __builtin_bit_cast(uint32_t, lo);
       aw[2 * d + 1] = __builtin_bit_cast(uint32_t, hi);
     }
-    if constexpr (is_fp8(BT)) {
-#pragma unroll
-      for (int d = 0; d < 4; ++d) {
-        bf16x2 lo, hi;
-        fp8x4_to_bf16<BT>(xc[u].w[d] & keep, lo, hi);
-        bw[2 * d] = __builtin_bit_cast(uint32_t, lo);
-        bw[2 * d + 1] = __builtin_bit_cast(uint32_t, hi);
-      }
-    } else {
-#pragma unroll
-      for (int d = 0; d < 8; ++d) bw[d] = xc[u].w[d] & keep;
-    }
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
+      const u32x4 xb = xslice_frag<BT, U>(xs, r, g, u, h);
       const u32x4 av = {aw[4 * h], aw[4 * h + 1], aw[4 * h + 2], aw[4 * h + 3]};
-      const u32x4 bv = {bw[4 * h], bw[4 * h + 1], bw[4 * h + 2], bw[4 * h + 3]};
+      const u32x4 bv = {xb[0] & xkeep, xb[1] & xkeep, xb[2] & xkeep, xb[3] & xkeep};
       acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, av), __builtin_bit_cast(bf16x8, bv), acc,
                                                     0, 0, 0);
     }
@@ -523,6 +593,10 @@ __device__ __forceinline__ void gemv_mfma_batch(const uint8_t *arow, const uint8
 template <int AT, int BT, int NB, int U>
 __global__ __launch_bounds__(kMThreads) void gemv_mfma_kernel(const uint8_t *A, long long lda, const uint8_t *B,
                                                              long long ldb, int m, int k, Epilogue e) {
+  using X = XSlice<BT, U>;
+  using W = WSlice<U>;
+  constexpr int kSlot = W::kBytes + X::kBytes;  // one batch of one wave in LDS: weights, then x
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[kMWaves][2][kSlot];
   __shared__ float part[kMWaves][16][17];
   __shared__ float red[kMWaves];
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -532,12 +606,33 @@ __global__ __launch_bounds__(kMThreads) void gemv_mfma_kernel(const uint8_t *A, 
   const EpiState st = epi_begin(e);
   GemvOut<NB> out;
   out.fetch(e, st, i0, m, 16, tid);
-  const uint8_t *arow = A + (long long)min(i0 + r, m - 1) * lda;  // rows past m: never stored
   const bool xlane = r < NB;
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  for (int cw = wave * 4 * U; cw < nch; cw += kMWaves * 4 * U) {
-    if (cw + 4 * U <= nch) gemv_mfma_batch<AT, BT, U, true>(arow, B, ldb, r, xlane, cw + g, nch, acc);
-    else gemv_mfma_batch<AT, BT, U, false>(arow, B, ldb, r, xlane, cw + g, nch, acc);
+  // Batches b = 0, 1, ... of this wave at chunks cw0 + b kStep (the last may be partial), both operands
+  // staged in this wave's two LDS slots by direct-to-LDS loads one batch ahead of the products.  Those
+  // loads are inline asm, invisible to the compiler, and no other vector-memory load is in the loop:
+  // the explicit wait before each batch (everything but the next batch's loads landed) is the only one.
+  constexpr int kStep = kMWaves * 4 * U, kPerBatch = W::kLoads + X::loads_for(NB);
+  const int cw0 = wave * 4 * U;
+  const int nb = cw0 < nch ? (nch - 1 - cw0) / kStep + 1 : 0;
+  if (nb > 0) {
+    wslice_issue<U>(lds[wave][0], A, lda, i0, m, cw0, nch, lane);
+    xslice_issue<BT, U, NB>(lds[wave][0] + W::kBytes, B, ldb, NB, cw0, nch, lane);
+  }
+  for (int b = 0; b < nb; ++b) {
+    const int cw = cw0 + b * kStep;
+    uint8_t *slot = lds[wave][b & 1];
+    if (b + 1 < nb) {
+      // the other slot was last read by batch b - 1, whose products are done
+      uint8_t *next = lds[wave][(b + 1) & 1];
+      wslice_issue<U>(next, A, lda, i0, m, cw + kStep, nch, lane);
+      xslice_issue<BT, U, NB>(next + W::kBytes, B, ldb, NB, cw + kStep, nch, lane);
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kPerBatch) : "memory");
+    } else {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
+    if (cw + 4 * U <= nch) gemv_mfma_compute<AT, BT, U, true>(slot, slot + W::kBytes, r, g, xlane, cw + g, nch, acc);
+    else gemv_mfma_compute<AT, BT, U, false>(slot, slot + W::kBytes, r, g, xlane, cw + g, nch, acc);
   }
   // lane l holds outputs (row 4 g + q, column r) of its wave's partial result
 #pragma unroll
@@ -558,7 +653,7 @@ __global__ __launch_bounds__(kMThreads) void gemv_mfma_kernel(const uint8_t *A, 
 template <int AT, int BT, int NB>
 hipError_t gemv_n(const uint8_t *A, long long lda, const uint8_t *B, long long ldb, int m, int k, const Epilogue &e,
                   hipStream_t s) {
-  if constexpr (BT != E5MA_FP32 && NB >= 5) {
+  if constexpr (BT != E5MA_FP32 && NB >= E5MA_GEMV_MFMA_MIN_N) {
     gemv_mfma_kernel<AT, BT, NB, E5MA_GEMV_MFMA_U><<<(m + 15) / 16, kMThreads, 0, s>>>(A, lda, B, ldb, m, k, e);
     return hipGetLastError();
   }
