@@ -10,6 +10,8 @@
 //   e5ma_tune [header] [--dry-run]       tune, print the entry, and (unless --dry-run) rewrite header
 //   e5ma_tune --emit header arch cus splitk_div cast_grid adam_grid_bf16 adam_grid_fp32 quant_grid [name]
 //                                        rewrite header with that entry, no device use (tests)
+//   e5ma_tune --ceiling                  AdamW over 2^28 parameters beside a kernel with the same memory
+//                                        accesses and no arithmetic (the access pattern's own ceiling)
 //
 // Workloads (the BASELINE shapes of each choice):
 //   cast_grid       FP32 -> E5M2 cast of 8192^2 elements, two sources rotated past the Infinity Cache
@@ -90,6 +92,77 @@ static std::vector<uint8_t> fetch(const void *p, size_t bytes) {
   std::vector<uint8_t> h(bytes);
   check(hipMemcpy(h.data(), p, bytes, hipMemcpyDeviceToHost), "hipMemcpy");
   return h;
+}
+
+// AdamW's memory accesses without its arithmetic: per thread and step 8 elements of g, p, m and v read
+// and p, m, v written back (16-byte accesses, non-temporal when NT, as adam.hip issues them for that
+// state width) plus 8 FP8 bytes, over the same grid-stride loop.  What is stored depends on what was
+// loaded (a xor), so no access is dropped.
+template <int ES, bool NT>
+__global__ __launch_bounds__(256) void stream_kernel(size_t count, uint8_t *p, const uint8_t *g, uint8_t *m,
+                                                     uint8_t *v, uint8_t *q) {
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  constexpr int kQ = 8 * ES / 16;  // 16-byte accesses per stream and step
+  const size_t tid = (size_t)blockIdx.x * 256 + threadIdx.x, stride = (size_t)gridDim.x * 256;
+  for (size_t c = tid; c < count / 8; c += stride) {
+    u32x4 G[kQ], P[kQ], M[kQ], V[kQ];
+#pragma unroll
+    for (int k = 0; k < kQ; ++k) {
+      const size_t o = c * kQ + k;
+      G[k] = NT ? __builtin_nontemporal_load((const u32x4 *)g + o) : ((const u32x4 *)g)[o];
+      P[k] = NT ? __builtin_nontemporal_load((const u32x4 *)p + o) : ((const u32x4 *)p)[o];
+      M[k] = NT ? __builtin_nontemporal_load((const u32x4 *)m + o) : ((const u32x4 *)m)[o];
+      V[k] = NT ? __builtin_nontemporal_load((const u32x4 *)v + o) : ((const u32x4 *)v)[o];
+    }
+    uint32_t h = 0;
+#pragma unroll
+    for (int k = 0; k < kQ; ++k) {
+      const size_t o = c * kQ + k;
+      const u32x4 pn = P[k] ^ G[k], mn = M[k] ^ G[k], vn = V[k] ^ G[k];
+      h ^= pn[0] ^ pn[1] ^ pn[2] ^ pn[3];
+      if constexpr (NT) {
+        __builtin_nontemporal_store(pn, (u32x4 *)p + o);
+        __builtin_nontemporal_store(mn, (u32x4 *)m + o);
+        __builtin_nontemporal_store(vn, (u32x4 *)v + o);
+      } else {
+        ((u32x4 *)p)[o] = pn;
+        ((u32x4 *)m)[o] = mn;
+        ((u32x4 *)v)[o] = vn;
+      }
+    }
+    *(uint2 *)(q + 8 * c) = make_uint2(h, h >> 8);
+  }
+}
+
+// AdamW (the library's kernel, the device's tuned grid) and stream_kernel on 2^28 parameters per state
+// width; rates in algorithmic bytes: n * (4 reads + 3 writes of the state width + 1 FP8 byte)
+static int ceiling(const DeviceInfo &di) {
+  const size_t n = (size_t)1 << 28;
+  for (int pt : {E5MA_BF16, E5MA_FP32}) {
+    const size_t es = pt == E5MA_BF16 ? 2 : 4, bytes = n * (7 * es + 1);
+    void *p = dalloc(n * es, 0x3C), *g = dalloc(n * es, 0x3A), *m = dalloc(n * es, 0x38), *v = dalloc(n * es, 0x30);
+    uint8_t *q = (uint8_t *)dalloc(n, 0);
+    AdamCoefficients a{};
+    a.lr = 1e-4f; a.b1 = 0.9f; a.b2 = 0.999f; a.c1 = 0.1f; a.c2 = 0.001f; a.corr1 = 1.f; a.corr2 = 1.f;
+    a.eps = 1e-8f; a.decay = 1e-6f; a.l2 = 0.01f; a.grad_mul = 1.f; a.decoupled = 1;
+    const int grid = pt == E5MA_BF16 ? di.tune.adam_grid_bf16 : di.tune.adam_grid_fp32;
+    const float adam = best_ms([&](int) {
+      return launch_adam(a, n, pt, p, pt, g, pt, m, v, E5MA_E5M2, q, nullptr, nullptr, di.tune, nullptr);
+    }, 3);
+    const float stream = best_ms([&](int) {
+      if (pt == E5MA_BF16)
+        stream_kernel<2, true><<<grid, 256>>>(n, (uint8_t *)p, (const uint8_t *)g, (uint8_t *)m, (uint8_t *)v, q);
+      else
+        stream_kernel<4, false><<<grid, 256>>>(n, (uint8_t *)p, (const uint8_t *)g, (uint8_t *)m, (uint8_t *)v, q);
+      return hipGetLastError();
+    }, 3);
+    printf("%s state, 2^28 parameters, grid %d: adam_kernel %.4f ms = %.1f GB/s; stream_kernel (same accesses, "
+           "no arithmetic) %.4f ms = %.1f GB/s; adam / stream = %.3f\n",
+           pt == E5MA_BF16 ? "BF16" : "FP32", grid, adam, bytes / (adam * 1e-3) / 1e9, stream,
+           bytes / (stream * 1e-3) / 1e9, stream / adam);
+    for (void *b : {p, g, m, v, (void *)q}) check(hipFree(b), "hipFree");
+  }
+  return 0;
 }
 
 static Tuning tune_device(const DeviceInfo &di) {
@@ -264,9 +337,10 @@ int main(int argc, char **argv) {
     return emit(argv[2], argv[3], atoi(argv[4]), t, argc > 10 ? argv[10] : "unnamed device");
   }
   const char *path = "e5m2effma_amd/csrc/e5ma_tuned.h";
-  bool dry = false;
+  bool dry = false, ceil_only = false;
   for (int i = 1; i < argc; ++i) {
     if (strcmp(argv[i], "--dry-run") == 0) dry = true;
+    else if (strcmp(argv[i], "--ceiling") == 0) ceil_only = true;
     else path = argv[i];
   }
   check(hipSetDevice(0), "hipSetDevice");
@@ -286,6 +360,10 @@ int main(int argc, char **argv) {
   if (char *c = strchr(arch, ':')) *c = 0;
   char name[256];
   snprintf(name, sizeof name, "%s", p.name[0] ? p.name : "an unnamed device");  // empty without amdgpu.ids
+  if (ceil_only) {
+    printf("AdamW access-pattern ceiling on %s (%s, %d CUs)\n", name, arch, di.cus);
+    return ceiling(di);
+  }
   printf("tuning on %s (%s, %d CUs)\n", name, arch, di.cus);
   const Tuning t = tune_device(di);
   printf("entry: {\"%s\", %d, {%d, %d, %d, %d, %d}}\n", arch, di.cus, t.splitk_div, t.cast_grid, t.adam_grid_bf16,

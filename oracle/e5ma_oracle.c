@@ -380,8 +380,9 @@ static void *chain_worker(void *arg) {
   return NULL;
 }
 
-/* D rows [row0, row1) of the GEMM with the reference tiled kernel's ascending-k FFMA chain;
- * columns split over nthreads POSIX threads.  Returns the updated amax. */
+/* D rows [row0, row1) of the GEMM with the reference tiled kernel's ascending-k FFMA chain, over
+ * nthreads POSIX threads: columns in groups of 8 split between them, or rows when there are fewer
+ * groups than threads (a GEMV).  Each output's chain is the same either way.  Returns the updated amax. */
 float orc_gemm_chain(const orc_gemm_args *g, float amax_in, int row0, int row1, int nthreads) {
   if (nthreads < 1) nthreads = 1;
   if (nthreads > 256) nthreads = 256;
@@ -389,13 +390,21 @@ float orc_gemm_chain(const orc_gemm_args *g, float amax_in, int row0, int row1, 
   if (row0 >= row1 || g->n <= 0) return amax_in;
   chain_job jobs[256];
   pthread_t th[256];
-  const int per = ((g->n + nthreads - 1) / nthreads + 7) / 8 * 8;
   int used = 0;
-  for (int t = 0; t < nthreads; ++t) {
-    const int j0 = t * per, j1 = j0 + per < g->n ? j0 + per : g->n;
-    if (j0 >= j1) break;
-    jobs[t] = (chain_job){g, row0, row1, j0, j1, 0.f};
-    ++used;
+  if ((g->n + 7) / 8 >= nthreads) {
+    const int per = ((g->n + nthreads - 1) / nthreads + 7) / 8 * 8;
+    for (int t = 0; t < nthreads; ++t) {
+      const int j0 = t * per, j1 = j0 + per < g->n ? j0 + per : g->n;
+      if (j0 >= j1) break;
+      jobs[used++] = (chain_job){g, row0, row1, j0, j1, 0.f};
+    }
+  } else {
+    const int rows = row1 - row0, per = (rows + nthreads - 1) / nthreads;
+    for (int t = 0; t < nthreads; ++t) {
+      const int r0 = row0 + t * per, r1 = r0 + per < row1 ? r0 + per : row1;
+      if (r0 >= r1) break;
+      jobs[used++] = (chain_job){g, r0, r1, 0, g->n, 0.f};
+    }
   }
   for (int t = 1; t < used; ++t) pthread_create(&th[t], NULL, chain_worker, &jobs[t]);
   if (used) chain_worker(&jobs[0]);

@@ -565,3 +565,18 @@ def test_lane_gemm_matches_reference_lane_and_closed_form(orc):
     one = orc.lane_gemm(a1, b1, M, N, K, 1, 1)
     prod = np.outer(orc.decode(4, a[:M]).astype(np.float64), orc.decode(4, b[:N]).astype(np.float64))
     assert np.array_equal(one, orc.encode(1, prod.astype(np.float32)).reshape(M, N))
+
+
+@pytest.mark.parametrize("n", [1, 8, 40])
+def test_chain_is_independent_of_the_thread_split(orc, n):
+    """The CPU chain splits columns, or rows for a GEMV; every output's chain is the same either way."""
+    rng = np.random.default_rng(60 + n)
+    M, K = 96, 256
+    a = orc.encode(orc.E5M2, (rng.standard_normal(M * K) * 2).astype(np.float32))
+    b = orc.encode(orc.BF16, rng.standard_normal(K * n).astype(np.float32))
+    outs = []
+    for th in (1, 5):
+        g = orc.Gemm(1, 0, M, n, K, 1.0, orc.E5M2, a, K, orc.BF16, b, K, ddt=orc.FP32)
+        g.chain(threads=th)
+        outs.append(g.D.copy())
+    assert np.array_equal(outs[0], outs[1])
