@@ -122,6 +122,29 @@ __device__ __forceinline__ void store_any(int t, void *p, size_t i, float v, flo
     default: store_t<E5MA_FP32>(p, i, v, qscale); break;
   }
 }
+// Four consecutive elements i .. i + 3 of dtype T (4-element aligned) in one vector store
+template <int T> __device__ __forceinline__ void store4_t(void *p, size_t i, const float (&v)[4], float qscale) {
+  uint8_t *dp = (uint8_t *)p + i * elem_bytes(T);
+  if constexpr (T == E5MA_FP32) {
+    *(float4 *)dp = make_float4(v[0], v[1], v[2], v[3]);
+  } else if constexpr (is_fp8(T)) {
+    *(uint32_t *)dp = encode_t<T>(v[0], qscale) | encode_t<T>(v[1], qscale) << 8 | encode_t<T>(v[2], qscale) << 16 |
+                      encode_t<T>(v[3], qscale) << 24;
+  } else {
+    *(uint2 *)dp = make_uint2(encode_t<T>(v[0], qscale) | encode_t<T>(v[1], qscale) << 16,
+                              encode_t<T>(v[2], qscale) | encode_t<T>(v[3], qscale) << 16);
+  }
+}
+// the same with the dtype chosen at run time (one dispatch per four elements)
+__device__ __forceinline__ void store4_any(int t, void *p, size_t i, const float (&v)[4], float qscale) {
+  switch (t) {
+    case E5MA_E5M2: store4_t<E5MA_E5M2>(p, i, v, qscale); break;
+    case E5MA_E4M3: store4_t<E5MA_E4M3>(p, i, v, qscale); break;
+    case E5MA_BF16: store4_t<E5MA_BF16>(p, i, v, qscale); break;
+    case E5MA_FP16: store4_t<E5MA_FP16>(p, i, v, qscale); break;
+    default: store4_t<E5MA_FP32>(p, i, v, qscale); break;
+  }
+}
 
 // ---- amax ---------------------------------------------------------------------------------------
 // Folds |v| into a running maximum, ignoring every NaN (quiet or signalling): the comparison is false

@@ -42,6 +42,8 @@ struct Tuning {
   int adam_grid_bf16 = 65536;  // block cap of the Adam kernel with BF16 parameters
   int adam_grid_fp32 = 8192;   // ... with FP32 parameters
   int quant_grid = 8192;       // block cap of the per-tensor quantize's amax pass (its cast pass: cast_grid)
+  int tail_half = 0;           // FP8 GEMM: 1 runs a last round of at most CUs / 2 tiles as 256 x 128 half tiles
+                               // (the same bits either way; measured slower on the MI355X, so 0 there)
 };
 
 struct DeviceInfo {

@@ -155,38 +155,43 @@ template <bool KC, bool PAIR, int J> __device__ __forceinline__ v8i read_frag(co
   }
 }
 
-// One unit: 16 MFMAs on fragment set P.
+// One unit: 4 NY MFMAs on fragment set P (NY = 4: a wave owns 128 x 128 of a 256 x 256 tile; NY = 2:
+// 128 x 64 of a 256 x 128 half tile, accumulator blocks y < 2).
 // BAR: starts with wait_barrier<WAITN, LGK>.
-// NEXT: the next unit's fragments (ring slot NS, unit NJ of that stage) are read into set 1 - P, one
-//   every second MFMA in the order its MFMAs use them (its first four need a0 and all of b): a0, b0,
-//   b1, b2, b3, a1, a2, a3.
-// ISSUE: stage ls's loads go into ring slot IS, one pair (A, B) after every (16 / kLoads)-th MFMA.
+// NEXT: the next unit's fragments (ring slot NS, unit NJ of that stage) are read into set 1 - P in the
+//   order its MFMAs use them (its first NY need a0 and all of b): a0, b0 .. b(NY - 1), a1, a2, a3, one
+//   every second MFMA (NY = 4) or every MFMA (NY = 2).
+// ISSUE: stage ls's loads go into ring slot IS, one pair (A, B) after every (4 NY / kLoads)-th MFMA.  A
+//   half tile issues every load of a whole tile (the B rows it does not use included), so that every
+//   wait count is the same for both widths.
 template <bool PAIR, int P, bool BAR, int WAITN, int LGK, bool NEXT, int NS, int NJ, bool ISSUE, int IS, int AT,
-          int BT, bool AKC, bool BKC>
+          int BT, bool AKC, bool BKC, int NY>
 __device__ __forceinline__ void f8_unit(const Loads<PAIR> &L, int ls, int lane, int wm, int wn, v8i (&a)[2][4],
                                         v8i (&b)[2][4], v16f (&acc)[4][4]) {
   using G = Ring<PAIR>;
-  constexpr int Q = 1 - P, kEvery = 16 / G::kLoads;
+  constexpr int Q = 1 - P, kMf = 4 * NY, kEvery = kMf / G::kLoads, kAt = kEvery > 1 ? 1 : 0;
+  constexpr int kFragStep = NY == 4 ? 2 : 1;  // MFMAs per fragment read
+  static_assert(kMf % G::kLoads == 0, "whole loads per unit");
   if constexpr (BAR) wait_barrier<WAITN, LGK>();
   const uint8_t *na = G::template slot_a<NS>(), *nb = G::template slot_b<NS>();
 #pragma unroll
   for (int x = 0; x < 4; ++x) {
 #pragma unroll
-    for (int y = 0; y < 4; ++y) {
+    for (int y = 0; y < NY; ++y) {
       // scale operands 0 select the unscaled v_mfma_f32_32x32x64_f8f6f4 (same products as the scaled form
       // with the neutral scale 127, one instruction dword pair shorter)
       acc[x][y] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a[P][x], b[P][y], acc[x][y], kMfmaFmt<AT>,
                                                                   kMfmaFmt<BT>, 0, 0, 0, 0);
-      const int i = 4 * x + y;
+      const int i = NY * x + y;
       if constexpr (ISSUE) {
-        if (i % kEvery == 1) issue_load<IS, PAIR>(L, ls, i / kEvery);
+        if (i % kEvery == kAt) issue_load<IS, PAIR>(L, ls, i / kEvery);
       }
       if constexpr (NEXT) {
-        if ((i & 1) == 0) {
-          const int f = i >> 1;
-          if (f >= 1 && f <= 4) b[Q][f - 1] = read_frag<BKC, PAIR, NJ>(nb, 128 * wn + 32 * (f - 1), lane);
+        if (i % kFragStep == 0 && i / kFragStep < 4 + NY) {
+          const int f = i / kFragStep;
+          if (f >= 1 && f <= NY) b[Q][f - 1] = read_frag<BKC, PAIR, NJ>(nb, 32 * NY * wn + 32 * (f - 1), lane);
           else {
-            const int fa = f == 0 ? 0 : f - 4;
+            const int fa = f == 0 ? 0 : f - NY;
             a[Q][fa] = read_frag<AKC, PAIR, NJ>(na, 128 * wm + 32 * fa, lane);
           }
         }
@@ -194,20 +199,26 @@ __device__ __forceinline__ void f8_unit(const Loads<PAIR> &L, int ls, int lane, 
     }
   }
   if constexpr (NEXT) {
-    // keep the LDS reads spread over the MFMA stream: MFMA, DS read, MFMA, DS read, ...
+    // keep the LDS reads spread over the MFMA stream: MFMA, DS read(s), MFMA, DS read(s), ...
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
+    for (int i = 0; i < kMf; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, NY == 4 ? 1 : 2, 0);
     }
   }
 }
 
+// LDS reads one unit issues for the next (2 per K-contiguous fragment, 4 per M / N-contiguous one)
+template <bool AKC, bool BKC, int NY> constexpr int kUnitReads = 4 * (AKC ? 2 : 4) + NY * (BKC ? 2 : 4);
+
 // The K loop of one block (nk units of 64 K) with the 4-slot ring: unit s is stage s in slot s % 4
-template <int AT, int BT, bool AKC, bool BKC>
+template <int AT, int BT, bool AKC, bool BKC, int NY>
 __device__ __forceinline__ void k_loop(const Loads<false> &L, int nk, int lane, int wm, int wn, v8i (&a)[2][4],
                                        v8i (&b)[2][4], v16f (&acc)[4][4]) {
   constexpr int W = Ring<false>::kW1;
+  // the barrier before unit s completes the reads of stage s - 1's fragments (issued during unit s - 2),
+  // not all of stage s's (issued during unit s - 1): at most one unit's reads stay outstanding
+  constexpr int kLgk = kUnitReads<AKC, BKC, NY> < 15 ? kUnitReads<AKC, BKC, NY> : 15;
   // stages 0..2 in flight; stage 0's fragments once it has landed
   issue_stage<0, false>(L, 0);
   issue_stage<1, false>(L, 1);
@@ -216,25 +227,25 @@ __device__ __forceinline__ void k_loop(const Loads<false> &L, int nk, int lane, 
 #pragma unroll
   for (int x = 0; x < 4; ++x) {
     a[0][x] = read_frag<AKC, false, 0>(lds_a<0>(), 128 * wm + 32 * x, lane);
-    b[0][x] = read_frag<BKC, false, 0>(lds_b<0>(), 128 * wn + 32 * x, lane);
+    if (x < NY) b[0][x] = read_frag<BKC, false, 0>(lds_b<0>(), 32 * NY * wn + 32 * x, lane);
   }
   // four stages per iteration, each awaiting s + 1 (s + 2 in flight) and issuing s + 3; then the last
   // four drain the ring (nk % 4 == 0, nk >= 8)
   int s = 0;
   for (; s < nk - 4; s += 4) {
-    f8_unit<false, 0, true, W, 15, true, 1, 0, true, 3, AT, BT, AKC, BKC>(L, s + 3, lane, wm, wn, a, b, acc);
-    f8_unit<false, 1, true, W, 15, true, 2, 0, true, 0, AT, BT, AKC, BKC>(L, s + 4, lane, wm, wn, a, b, acc);
-    f8_unit<false, 0, true, W, 15, true, 3, 0, true, 1, AT, BT, AKC, BKC>(L, s + 5, lane, wm, wn, a, b, acc);
-    f8_unit<false, 1, true, W, 15, true, 0, 0, true, 2, AT, BT, AKC, BKC>(L, s + 6, lane, wm, wn, a, b, acc);
+    f8_unit<false, 0, true, W, kLgk, true, 1, 0, true, 3, AT, BT, AKC, BKC, NY>(L, s + 3, lane, wm, wn, a, b, acc);
+    f8_unit<false, 1, true, W, kLgk, true, 2, 0, true, 0, AT, BT, AKC, BKC, NY>(L, s + 4, lane, wm, wn, a, b, acc);
+    f8_unit<false, 0, true, W, kLgk, true, 3, 0, true, 1, AT, BT, AKC, BKC, NY>(L, s + 5, lane, wm, wn, a, b, acc);
+    f8_unit<false, 1, true, W, kLgk, true, 0, 0, true, 2, AT, BT, AKC, BKC, NY>(L, s + 6, lane, wm, wn, a, b, acc);
   }
-  f8_unit<false, 0, true, W, 15, true, 1, 0, true, 3, AT, BT, AKC, BKC>(L, s + 3, lane, wm, wn, a, b, acc);
-  f8_unit<false, 1, true, W, 15, true, 2, 0, false, 0, AT, BT, AKC, BKC>(L, 0, lane, wm, wn, a, b, acc);
-  f8_unit<false, 0, true, 0, 15, true, 3, 0, false, 0, AT, BT, AKC, BKC>(L, 0, lane, wm, wn, a, b, acc);
-  f8_unit<false, 1, false, 0, 0, false, 0, 0, false, 0, AT, BT, AKC, BKC>(L, 0, lane, wm, wn, a, b, acc);
+  f8_unit<false, 0, true, W, kLgk, true, 1, 0, true, 3, AT, BT, AKC, BKC, NY>(L, s + 3, lane, wm, wn, a, b, acc);
+  f8_unit<false, 1, true, W, kLgk, true, 2, 0, false, 0, AT, BT, AKC, BKC, NY>(L, 0, lane, wm, wn, a, b, acc);
+  f8_unit<false, 0, true, 0, kLgk, true, 3, 0, false, 0, AT, BT, AKC, BKC, NY>(L, 0, lane, wm, wn, a, b, acc);
+  f8_unit<false, 1, false, 0, 0, false, 0, 0, false, 0, AT, BT, AKC, BKC, NY>(L, 0, lane, wm, wn, a, b, acc);
 }
 
 // The K loop with the 2-stage ring: stage p (units 2p, 2p + 1) in region p % 2
-template <int AT, int BT, bool AKC, bool BKC>
+template <int AT, int BT, bool AKC, bool BKC, int NY>
 __device__ __forceinline__ void k_loop(const Loads<true> &L, int nk, int lane, int wm, int wn, v8i (&a)[2][4],
                                        v8i (&b)[2][4], v16f (&acc)[4][4]) {
   constexpr int W = Ring<true>::kW1;
@@ -246,21 +257,21 @@ __device__ __forceinline__ void k_loop(const Loads<true> &L, int nk, int lane, i
 #pragma unroll
   for (int x = 0; x < 4; ++x) {
     a[0][x] = read_frag<AKC, true, 0>(lds_a<0>(), 128 * wm + 32 * x, lane);
-    b[0][x] = read_frag<BKC, true, 0>(lds_b<0>(), 128 * wn + 32 * x, lane);
+    if (x < NY) b[0][x] = read_frag<BKC, true, 0>(lds_b<0>(), 32 * NY * wn + 32 * x, lane);
   }
   // two stages (one per region) per iteration, each issuing stage p + 2 in its second unit; then the
   // last two stages
   int p = 0;
   for (; p < np - 2; p += 2) {
-    f8_unit<true, 0, false, 0, 0, true, 0, 1, false, 0, AT, BT, AKC, BKC>(L, 0, lane, wm, wn, a, b, acc);
-    f8_unit<true, 1, true, 0, 0, true, 1, 0, true, 0, AT, BT, AKC, BKC>(L, p + 2, lane, wm, wn, a, b, acc);
-    f8_unit<true, 0, false, 0, 0, true, 1, 1, false, 0, AT, BT, AKC, BKC>(L, 0, lane, wm, wn, a, b, acc);
-    f8_unit<true, 1, true, 0, 0, true, 0, 0, true, 1, AT, BT, AKC, BKC>(L, p + 3, lane, wm, wn, a, b, acc);
+    f8_unit<true, 0, false, 0, 0, true, 0, 1, false, 0, AT, BT, AKC, BKC, NY>(L, 0, lane, wm, wn, a, b, acc);
+    f8_unit<true, 1, true, 0, 0, true, 1, 0, true, 0, AT, BT, AKC, BKC, NY>(L, p + 2, lane, wm, wn, a, b, acc);
+    f8_unit<true, 0, false, 0, 0, true, 1, 1, false, 0, AT, BT, AKC, BKC, NY>(L, 0, lane, wm, wn, a, b, acc);
+    f8_unit<true, 1, true, 0, 0, true, 0, 0, true, 1, AT, BT, AKC, BKC, NY>(L, p + 3, lane, wm, wn, a, b, acc);
   }
-  f8_unit<true, 0, false, 0, 0, true, 0, 1, false, 0, AT, BT, AKC, BKC>(L, 0, lane, wm, wn, a, b, acc);
-  f8_unit<true, 1, true, 0, 0, true, 1, 0, false, 0, AT, BT, AKC, BKC>(L, 0, lane, wm, wn, a, b, acc);
-  f8_unit<true, 0, false, 0, 0, true, 1, 1, false, 0, AT, BT, AKC, BKC>(L, 0, lane, wm, wn, a, b, acc);
-  f8_unit<true, 1, false, 0, 0, false, 0, 0, false, 0, AT, BT, AKC, BKC>(L, 0, lane, wm, wn, a, b, acc);
+  f8_unit<true, 0, false, 0, 0, true, 0, 1, false, 0, AT, BT, AKC, BKC, NY>(L, 0, lane, wm, wn, a, b, acc);
+  f8_unit<true, 1, true, 0, 0, true, 1, 0, false, 0, AT, BT, AKC, BKC, NY>(L, 0, lane, wm, wn, a, b, acc);
+  f8_unit<true, 0, false, 0, 0, true, 1, 1, false, 0, AT, BT, AKC, BKC, NY>(L, 0, lane, wm, wn, a, b, acc);
+  f8_unit<true, 1, false, 0, 0, false, 0, 0, false, 0, AT, BT, AKC, BKC, NY>(L, 0, lane, wm, wn, a, b, acc);
 }
 
 template <int AT, int BT, bool AKC, bool BKC, int EPI>
@@ -286,23 +297,74 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_f8_kernel(TileArgs t, Epilog
       for (int r = 0; r < 16; ++r) acc[x][y][r] = 0.f;
   v8i a[2][4], b[2][4];  // fragments, double-buffered by unit parity
   const Loads<PAIR> L = make_loads<AKC, BKC, PAIR>(t, i0, j0, wave, lane);
-  k_loop<AT, BT, AKC, BKC>(L, t.k / kUnitK, lane, wm, wn, a, b, acc);
+  k_loop<AT, BT, AKC, BKC, 4>(L, t.k / kUnitK, lane, wm, wn, a, b, acc);
 
   const float mx = tile_epilogue<EPI>(t, e, acc, i0, j0, wm, wn, lane, tid, simple, vec, sa1, sb1);
   if (e.amax) amax_commit_block(e.amax, mx, red);
 }
 
+// A launch of 256 x 128 half tiles (block b: half b % 2 of tile first + b / 2): the same K loop with 128 x 64
+// per wave.  Each output's products accumulate in the same order as in a whole tile, so the results are the
+// same bits.  Used for a last round of tiles at most half as large as the CU count, whose half tiles then
+// fill the device.
 template <int AT, int BT, bool AKC, bool BKC>
-hipError_t run_d(const TileArgs &t, const Epilogue &e, hipStream_t s) {
-  const int grid = t.tiles_m * t.tiles_n * t.splits;
+__global__ __launch_bounds__(kThreads, 1) void gemm_f8_half_kernel(TileArgs t, Epilogue e, int vec) {
+  constexpr bool PAIR = BKC;
+  __shared__ float red[kThreads / 64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  int tm, tn, h;
+  tile_of_half(blockIdx.x, t, tm, tn, h);
+  const int i0 = tm * kBM, j0 = tn * kBN + 128 * h;
+  if (j0 >= t.n) return;  // the right half of a tile narrower than 129 columns: nothing to do (whole block)
+
+  v16f acc[4][4];
+#pragma unroll
+  for (int x = 0; x < 4; ++x)
+#pragma unroll
+    for (int y = 0; y < 4; ++y)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[x][y][r] = 0.f;
+  v8i a[2][4], b[2][4];
+  const Loads<PAIR> L = make_loads<AKC, BKC, PAIR>(t, i0, j0, wave, lane);
+  k_loop<AT, BT, AKC, BKC, 2>(L, t.k / kUnitK, lane, wm, wn, a, b, acc);
+
+  __builtin_amdgcn_sched_barrier(0);
+  const float mx = half_tile_epilogue(t, e, acc, i0, j0, wm, wn, lane, tid, vec);
+  if (e.amax) amax_commit_block(e.amax, mx, red);
+}
+
+// tail_cus > 0 (unsplit launches only): when the last round of tiles over that many CUs is at most half
+// full, the whole rounds run as one launch and the last round's tiles as a launch of half tiles
+template <int AT, int BT, bool AKC, bool BKC>
+hipError_t run_d(const TileArgs &t0, const Epilogue &e, int tail_cus, hipStream_t s) {
+  TileArgs t = t0;
+  const int tiles = t.tiles_m * t.tiles_n;
+  int whole = tiles * t.splits, tail = 0;
+  if (tail_cus > 0 && t.splits == 1) {
+    const int rounds = (tiles + tail_cus - 1) / tail_cus, last = tiles - (rounds - 1) * tail_cus;
+    if (2 * last <= tail_cus) {
+      whole = (rounds - 1) * tail_cus;
+      tail = last;
+    }
+  }
   // the staged epilogues write 4-element groups of D and read OUTER scales of A as 16-byte vectors
   const int vec = ((uintptr_t)e.d % (4 * elem_bytes(e.d_dtype))) == 0 && e.ldd % 4 == 0 &&
                   (!e.sa_vec || (uintptr_t)e.sa % 16 == 0);
   const int simple = e.bias == nullptr && e.beta == 0.f && vec;
-  switch (epilogue_class(t.m, t.n, e, simple, vec)) {  // D's dtype is a run-time choice of the epilogue
-    case kEpiFast16: gemm_f8_kernel<AT, BT, AKC, BKC, kEpiFast16><<<grid, kThreads, 0, s>>>(t, e, simple, vec); break;
-    case kEpiFull: gemm_f8_kernel<AT, BT, AKC, BKC, kEpiFull><<<grid, kThreads, 0, s>>>(t, e, simple, vec); break;
-    default: gemm_f8_kernel<AT, BT, AKC, BKC, kEpiAny><<<grid, kThreads, 0, s>>>(t, e, simple, vec); break;
+  if (whole > 0) {
+    t.first = 0;
+    t.count = whole;
+    switch (epilogue_class(t.m, t.n, e, simple, vec)) {  // D's dtype is a run-time choice of the epilogue
+      case kEpiFast16: gemm_f8_kernel<AT, BT, AKC, BKC, kEpiFast16><<<whole, kThreads, 0, s>>>(t, e, simple, vec); break;
+      case kEpiFull: gemm_f8_kernel<AT, BT, AKC, BKC, kEpiFull><<<whole, kThreads, 0, s>>>(t, e, simple, vec); break;
+      default: gemm_f8_kernel<AT, BT, AKC, BKC, kEpiAny><<<whole, kThreads, 0, s>>>(t, e, simple, vec); break;
+    }
+  }
+  if (tail > 0) {
+    t.first = whole;
+    t.count = tail;
+    gemm_f8_half_kernel<AT, BT, AKC, BKC><<<2 * tail, kThreads, 0, s>>>(t, e, vec);
   }
   return hipGetLastError();
 }
@@ -311,12 +373,15 @@ hipError_t run_d(const TileArgs &t, const Epilogue &e, hipStream_t s) {
 // the FP32 partial output of split 0 (the next split's follows at e.ldd * n floats)
 template <bool AKC, bool BKC>
 hipError_t launch_layout(int at, int bt, const uint8_t *A, long long lda, const uint8_t *B, long long ldb, int m, int n,
-                         int k, int splits, const Epilogue &e, hipStream_t s) {
-  const int ks = k / splits;
-  TileArgs t{A, B, lda, ldb, m, n, ks, (m + kBM - 1) / kBM, (n + kBN - 1) / kBN, splits,
-             AKC ? ks : ks * lda, BKC ? ks : ks * ldb, e.ldd * n * 4};
-  if (at == E5MA_E5M2) return bt == E5MA_E5M2 ? run_d<E5MA_E5M2, E5MA_E5M2, AKC, BKC>(t, e, s) : run_d<E5MA_E5M2, E5MA_E4M3, AKC, BKC>(t, e, s);
-  return bt == E5MA_E5M2 ? run_d<E5MA_E4M3, E5MA_E5M2, AKC, BKC>(t, e, s) : run_d<E5MA_E4M3, E5MA_E4M3, AKC, BKC>(t, e, s);
+                         int k, int splits, int tail_cus, const Epilogue &e, hipStream_t s) {
+  const int ks = k / splits, tm = (m + kBM - 1) / kBM, tn = (n + kBN - 1) / kBN;
+  const TileArgs t{A, B, lda, ldb, m, n, ks, tm, tn, splits, AKC ? ks : ks * lda, BKC ? ks : ks * ldb, e.ldd * n * 4,
+                   0, tm * tn * splits};
+  if (at == E5MA_E5M2)
+    return bt == E5MA_E5M2 ? run_d<E5MA_E5M2, E5MA_E5M2, AKC, BKC>(t, e, tail_cus, s)
+                           : run_d<E5MA_E5M2, E5MA_E4M3, AKC, BKC>(t, e, tail_cus, s);
+  return bt == E5MA_E5M2 ? run_d<E5MA_E4M3, E5MA_E5M2, AKC, BKC>(t, e, tail_cus, s)
+                         : run_d<E5MA_E4M3, E5MA_E4M3, AKC, BKC>(t, e, tail_cus, s);
 }
 
 }  // namespace f8k

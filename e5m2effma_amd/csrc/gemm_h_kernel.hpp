@@ -258,8 +258,9 @@ template <bool AKC, bool BKC>
 hipError_t launch_layout(int at, int bt, const uint8_t *A, long long lda, const uint8_t *B, long long ldb, int m, int n,
                          int k, int splits, const Epilogue &e, hipStream_t s) {
   const int ks = k / splits;
-  TileArgs t{A, B, lda, ldb, m, n, ks, (m + kBM - 1) / kBM, (n + kBN - 1) / kBN, splits,
-             AKC ? ks : ks * lda, BKC ? ks : ks * ldb, e.ldd * n * 4};
+  const int tm = (m + kBM - 1) / kBM, tn = (n + kBN - 1) / kBN;
+  const TileArgs t{A, B, lda, ldb, m, n, ks, tm, tn, splits, AKC ? ks : ks * lda, BKC ? ks : ks * ldb, e.ldd * n * 4,
+                   0, tm * tn * splits};
   if (at == E5MA_E5M2)
     return bt == E5MA_E5M2 ? run_d<E5MA_E5M2, E5MA_E5M2, AKC, BKC>(t, e, s) : run_d<E5MA_E5M2, E5MA_E4M3, AKC, BKC>(t, e, s);
   return bt == E5MA_E5M2 ? run_d<E5MA_E4M3, E5MA_E5M2, AKC, BKC>(t, e, s) : run_d<E5MA_E4M3, E5MA_E4M3, AKC, BKC>(t, e, s);
@@ -270,8 +271,9 @@ template <bool AKC>
 hipError_t launch_layout_bf16(int at, int, const uint8_t *A, long long lda, const uint8_t *B, long long ldb, int m, int n,
                               int k, int splits, const Epilogue &e, hipStream_t s) {
   const int ks = k / splits;
-  TileArgs t{A, B, lda, 2 * ldb, m, n, ks, (m + kBM - 1) / kBM, (n + kBN - 1) / kBN, splits,
-             AKC ? ks : ks * lda, 2LL * ks, e.ldd * n * 4};
+  const int tm = (m + kBM - 1) / kBM, tn = (n + kBN - 1) / kBN;
+  const TileArgs t{A, B, lda, 2 * ldb, m, n, ks, tm, tn, splits, AKC ? ks : ks * lda, 2LL * ks, e.ldd * n * 4,
+                   0, tm * tn * splits};
   return at == E5MA_E5M2 ? run_d<E5MA_E5M2, E5MA_BF16, AKC, true>(t, e, s) : run_d<E5MA_E4M3, E5MA_BF16, AKC, true>(t, e, s);
 }
 

@@ -62,6 +62,7 @@ struct TileArgs {
   int splits;                 // K splits (1: none); split s writes FP32 partials at D + s * d_split
   long long a_split, b_split;  // bytes from one split's first A / B element to the next split's
   long long d_split;          // bytes between the splits' partial outputs
+  int first, count;           // this launch's (tile, split) indices: first .. first + count - 1
 };
 
 // Output tile and K split of block b.  XCD-aware when the block count is a multiple of 8 (blocks are
@@ -69,11 +70,28 @@ struct TileArgs {
 // works on one split (one K slice of the operands in its L2); then tiles are grouped kGroupM m-tiles
 // at a time.
 __device__ __forceinline__ void tile_of(int b, const TileArgs &t, int &tm, int &tn, int &split) {
-  const int tiles = t.tiles_m * t.tiles_n, total = tiles * t.splits;
+  const int tiles = t.tiles_m * t.tiles_n, total = t.count;
   int x = b;
   if ((total & 7) == 0) x = (b & 7) * (total >> 3) + (b >> 3);
+  x += t.first;
   split = x / tiles;
   x -= split * tiles;
+  const int per_group = kGroupM * t.tiles_n;
+  const int g = x / per_group, r = x - g * per_group;
+  const int gm = min(kGroupM, t.tiles_m - g * kGroupM);
+  tm = g * kGroupM + r % gm;
+  tn = r / gm;
+}
+
+// Half tile of block b of a launch of 256 x 128 half tiles (no K splits) over tiles first .. first + count - 1
+// in the same (m-grouped) order.  XCD-aware like tile_of when count is a multiple of 8: XCD b % 8 runs a
+// contiguous run of count / 8 tiles, both halves of each (half = index within the XCD % 2), so the tiles an
+// XCD runs at once share operand slices in its L2.
+__device__ __forceinline__ void tile_of_half(int b, const TileArgs &t, int &tm, int &tn, int &h) {
+  int q = b;  // position among the 2 count half tiles
+  if ((t.count & 7) == 0) q = (b & 7) * (t.count >> 2) + (b >> 3);
+  const int x = t.first + (q >> 1);
+  h = q & 1;
   const int per_group = kGroupM * t.tiles_n;
   const int g = x / per_group, r = x - g * per_group;
   const int gm = min(kGroupM, t.tiles_m - g * kGroupM);
@@ -145,6 +163,16 @@ template <int T> __device__ __forceinline__ void load4_t(const void *p, size_t i
     }
   }
 }
+// the same with the dtype chosen at run time (one dispatch per four elements)
+__device__ __forceinline__ void load4_any(int t, const void *p, size_t idx, float sinv, float (&o)[4]) {
+  switch (t) {
+    case E5MA_E5M2: load4_t<E5MA_E5M2>(p, idx, sinv, o); break;
+    case E5MA_E4M3: load4_t<E5MA_E4M3>(p, idx, sinv, o); break;
+    case E5MA_BF16: load4_t<E5MA_BF16>(p, idx, sinv, o); break;
+    case E5MA_FP16: load4_t<E5MA_FP16>(p, idx, sinv, o); break;
+    default: load4_t<E5MA_FP32>(p, idx, sinv, o); break;
+  }
+}
 
 // Writes out one staged half tile (256 rows x 128 columns starting at column jh) in the reference's
 // epilogue order (include/e5m2effma.h: v = acc * (alpha * sa[i]) * sb[j]; v += bias[i];
@@ -164,7 +192,9 @@ __device__ __forceinline__ float general_half(const Epilogue &e, const EpiState 
   const int w = tid >> 6, il = 4 * (tid & 63);
   const bool rows4 = i + 3 < t.m;
   bool cvec = false;
-  if constexpr (CT >= 0 && CT != kAnyC)
+  if constexpr (CT == kAnyC)
+    cvec = rows4 && e.beta != 0.f && (uintptr_t)e.c % (4 * elem_bytes(e.c_dtype)) == 0 && e.ldc % 4 == 0;
+  else if constexpr (CT >= 0)
     cvec = rows4 && (uintptr_t)e.c % (4 * elem_bytes(CT)) == 0 && e.ldc % 4 == 0;
   const float sb1 = scale_or_one(e.sb);
 #pragma unroll 1
@@ -179,9 +209,13 @@ __device__ __forceinline__ float general_half(const Epilogue &e, const EpiState 
       for (int q = 0; q < 4; ++q) cv[u][q] = 0.f;
       if constexpr (CT == kAnyC) {
         if (j < t.n && e.beta != 0.f) {  // beta = 0: there is no C (NULL), and none is read
+          if (cvec) {
+            load4_any(e.c_dtype, e.c, (size_t)j * e.ldc + i, st.csinv, cv[u]);
+          } else {
 #pragma unroll
-          for (int q = 0; q < 4; ++q)
-            if (i + q < t.m) cv[u][q] = load_any(e.c_dtype, e.c, (size_t)j * e.ldc + i + q, st.csinv);
+            for (int q = 0; q < 4; ++q)
+              if (i + q < t.m) cv[u][q] = load_any(e.c_dtype, e.c, (size_t)j * e.ldc + i + q, st.csinv);
+          }
         }
       } else if constexpr (CT >= 0) {
         if (j < t.n) {
@@ -213,12 +247,18 @@ __device__ __forceinline__ float general_half(const Epilogue &e, const EpiState 
       }
       const size_t o = (size_t)j * e.ldd + i;
       if constexpr (DT == kAnyD) {
+        if (rows4 && vec) {
+          store4_any(e.d_dtype, e.d, o, v, st.qscale);
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-          if (i + q < t.m) {
-            store_any(e.d_dtype, e.d, o + q, v[q], st.qscale);
-            mx = amax_fold(mx, v[q]);
-          }
+          for (int q = 0; q < 4; ++q) mx = amax_fold(mx, v[q]);
+        } else {
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            if (i + q < t.m) {
+              store_any(e.d_dtype, e.d, o + q, v[q], st.qscale);
+              mx = amax_fold(mx, v[q]);
+            }
+        }
         continue;
       } else if (rows4 && vec) {
         uint8_t *dp = (uint8_t *)e.d + o * elem_bytes(DT);
@@ -288,9 +328,11 @@ __shared__ int g_nan_flag;
 // payload: every lane folds 0 * v into a screen that is NaN exactly when some value is NaN or Inf, and a
 // block-wide flag then makes phase R rewrite NaN codes (rare path).
 // Phase R: step q writes tile columns 8q .. 8q + 7, thread t column 8q + t / 32, rows 8 (t % 32) .. + 7.
-template <int DT>
-__device__ __forceinline__ float staged16(const Epilogue &e, v16f (&acc)[4][4], int i0, int j0, int wm, int wn,
-                                          int lane, int tid, float sa1, float sb1) {
+// EDGE: the tile may reach past m or n (stores, scale reads and amax limited to D); false: a full tile,
+// no checks (the checks cost the 8192^3 GEMM 4 %).
+template <int DT, bool EDGE>
+__device__ __forceinline__ float staged16(const Epilogue &e, v16f (&acc)[4][4], int i0, int j0, int m, int n, int wm,
+                                          int wn, int lane, int tid, float sa1, float sb1) {
   static_assert(elem_bytes(DT) == 2, "2-byte outputs");
   float mx = 0.f;
   const float s = sa1 * sb1;
@@ -301,7 +343,8 @@ __device__ __forceinline__ float staged16(const Epilogue &e, v16f (&acc)[4][4], 
   __syncthreads();  // every wave has read its last fragments from the ring
 #pragma unroll
   for (int y = 0; y < 4; ++y) {
-    const float sbj = e.sb_vec ? e.sb[j0 + 128 * wn + 32 * y + lc] : sb1;
+    const int jc = j0 + 128 * wn + 32 * y + lc;  // this lane's column; past n (edge tiles) it is never stored
+    const float sbj = e.sb_vec ? e.sb[EDGE ? min(jc, n - 1) : jc] : sb1;
     uint8_t *col = (uint8_t *)stage_at(4 * wn + y) + lc * 512;
 #pragma unroll
     for (int x = 0; x < 4; ++x)
@@ -312,11 +355,13 @@ __device__ __forceinline__ float staged16(const Epilogue &e, v16f (&acc)[4][4], 
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
           const int g = 2 * p + h;
+          const int r4 = i0 + 128 * wm + 32 * x + 8 * g + 4 * hi;  // rows r4 .. r4 + 3
           float v[4];
           if (vs) {
             float as[4];
             if (e.sa_vec) {
-              const float4 a4 = *(const float4 *)(e.sa + i0 + 128 * wm + 32 * x + 8 * g + 4 * hi);
+              // rows past m (edge tiles; m % 8 == 0) read the last in-range group: never stored
+              const float4 a4 = *(const float4 *)(e.sa + (EDGE ? min(r4, m - 4) : r4));
               as[0] = e.alpha * a4.x; as[1] = e.alpha * a4.y; as[2] = e.alpha * a4.z; as[3] = e.alpha * a4.w;
             } else {
               as[0] = as[1] = as[2] = as[3] = sa1;
@@ -333,7 +378,8 @@ __device__ __forceinline__ float staged16(const Epilogue &e, v16f (&acc)[4][4], 
           }
           if (amax) {
 #pragma unroll
-            for (int q = 0; q < 4; ++q) mx = amax_fold(mx, v[q]);
+            for (int q = 0; q < 4; ++q)
+              if (!EDGE || (jc < n && r4 + q < m)) mx = amax_fold(mx, v[q]);
           }
           if constexpr (DT == E5MA_BF16) {
             typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
@@ -357,6 +403,7 @@ __device__ __forceinline__ float staged16(const Epilogue &e, v16f (&acc)[4][4], 
   __syncthreads();
   const bool fix = DT == E5MA_BF16 && g_nan_flag != 0;
   const int cq = tid >> 5, k = tid & 31;
+  const bool rowv = i0 + 8 * k < m;  // this thread's 8 rows: all below m or none (m % 8 == 0, class precondition)
   uint8_t *gp = (uint8_t *)e.d + ((size_t)(j0 + cq) * e.ldd + i0 + 8 * k) * 2;
   const size_t gstep = (size_t)16 * e.ldd;  // 8 columns
 #pragma unroll
@@ -367,7 +414,7 @@ __device__ __forceinline__ float staged16(const Epilogue &e, v16f (&acc)[4][4], 
       d.x = bf16_pair_canonical(d.x); d.y = bf16_pair_canonical(d.y);
       d.z = bf16_pair_canonical(d.z); d.w = bf16_pair_canonical(d.w);
     }
-    *(uint4 *)(gp + q * gstep) = d;
+    if (!EDGE || (rowv && j0 + 8 * q + cq < n)) *(uint4 *)(gp + q * gstep) = d;
   }
   return mx;
 }
@@ -382,18 +429,19 @@ __device__ __forceinline__ float staged16(const Epilogue &e, v16f (&acc)[4][4], 
 // (the order of include/e5m2effma.h).  C is loaded a group of 8 steps ahead of its use, the next half's
 // first group before that half is staged (a load waited on right away left the TE wgrad GEMM 17% slower).
 // C may alias D: each thread reads its own elements before it writes them, and no other thread writes them.
-template <int DT, int CT>
-__device__ __forceinline__ float staged_general(const Epilogue &e, v16f (&acc)[4][4], int i0, int j0, int wm,
-                                                int wn, int lane, int tid, float sa1, float sb1) {
+template <int DT, int CT, bool EDGE>
+__device__ __forceinline__ float staged_general(const Epilogue &e, v16f (&acc)[4][4], int i0, int j0, int m, int n,
+                                                int wm, int wn, int lane, int tid, float sa1, float sb1) {
   float mx = 0.f;
   const float s = sa1 * sb1;
   const bool vs = e.sa_vec || e.sb_vec;
   const int lc = lane & 15, hi = lane >> 5, kr = tid & 63, cq = tid >> 6;
-  const int i = i0 + 4 * kr;  // phase R rows i .. i + 3
+  const int i = i0 + 4 * kr;  // phase R rows i .. i + 3: all below m or none (m % 4 == 0, class precondition)
+  const bool rowv = i < m;
   float rb[4] = {0.f, 0.f, 0.f, 0.f};
   if (e.bias) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) rb[r] = load_any(e.bias_dtype, e.bias, (size_t)(i + r), 1.f);
+    for (int r = 0; r < 4; ++r) rb[r] = load_any(e.bias_dtype, e.bias, (size_t)(EDGE ? min(i + r, m - 1) : i + r), 1.f);
   }
   const float csinv = scale_or_one(e.c_sinv), qs = scale_or_one(e.d_scale);
   const bool amax = e.amax != nullptr;
@@ -405,12 +453,12 @@ __device__ __forceinline__ float staged_general(const Epilogue &e, v16f (&acc)[4
     for (int u = 0; u < 8; ++u) {
       const int q = 8 * (g & 3) + u;
       const int j = j0 + 128 * (g >> 2) + 4 * q + cq;
-      if constexpr (CT == kAnyC) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-          c[u][r] = e.beta != 0.f ? load_any(e.c_dtype, e.c, (size_t)j * e.ldc + i + r, csinv) : 0.f;
-      } else if constexpr (CT >= 0) {
-        load4_t<CT>(e.c, (size_t)j * e.ldc + i, csinv, c[u]);  // C 4-element aligned (class precondition)
+      for (int r = 0; r < 4; ++r) c[u][r] = 0.f;
+      // C exists for these elements (edge tiles: not past m or n); 4-element aligned (class precondition)
+      if ((!EDGE || (j < n && rowv)) && (CT != kAnyC || e.beta != 0.f)) {
+        if constexpr (CT == kAnyC) load4_any(e.c_dtype, e.c, (size_t)j * e.ldc + i, csinv, c[u]);
+        else if constexpr (CT >= 0) load4_t<CT>(e.c, (size_t)j * e.ldc + i, csinv, c[u]);
       }
     }
   };
@@ -437,14 +485,19 @@ __device__ __forceinline__ float staged_general(const Epilogue &e, v16f (&acc)[4
           v[r] = __builtin_fmaf(e.beta, cur[u][r], v[r]);
         }
       }
+      const bool valid = !EDGE || (j < n && rowv);  // edge tiles: these 4 outputs are inside D, or none is
       if (amax) {
+        if (valid) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) mx = amax_fold(mx, v[r]);
+          for (int r = 0; r < 4; ++r) mx = amax_fold(mx, v[r]);
+        }
         asm volatile("" : "+v"(mx));  // folded here: sunk to the end, it keeps every value alive (spills)
       }
+      if constexpr (EDGE) {
+        if (!valid) continue;
+      }
       if constexpr (DT == kAnyD) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) store_any(e.d_dtype, e.d, (size_t)j * e.ldd + i + r, v[r], qs);
+        store4_any(e.d_dtype, e.d, (size_t)j * e.ldd + i, v, qs);  // D 4-element aligned (class precondition)
       } else {
         uint8_t *dp = (uint8_t *)e.d + ((size_t)j * e.ldd + i) * elem_bytes(DT);
         if constexpr (DT == E5MA_FP32) {
@@ -469,7 +522,7 @@ __device__ __forceinline__ float staged_general(const Epilogue &e, v16f (&acc)[4
       for (int y = 0; y < 4; ++y) {
         const int c = 32 * y + (lane & 31);  // column within the half
         float sbj = sb1;
-        if (e.sb_vec) sbj = e.sb[j0 + 128 * h + c];
+        if (e.sb_vec) sbj = e.sb[EDGE ? min(j0 + 128 * h + c, n - 1) : j0 + 128 * h + c];  // past n: never stored
         // buffer c / 16 = 2 y + (lane & 16 ? 1 : 0): a select between two pointers, not a lane-indexed switch
         float *colp = ((lane & 16) ? stage_at(2 * y + 1) : stage_at(2 * y)) + lc * 256;
 #pragma unroll
@@ -482,7 +535,8 @@ __device__ __forceinline__ float staged_general(const Epilogue &e, v16f (&acc)[4
             if (vs) {
               float as[4];
               if (e.sa_vec) {
-                const float4 a4 = *(const float4 *)(e.sa + i0 + 4 * chunk);
+                // rows past m (edge tiles; m % 4 == 0) read the last in-range group: never stored
+                const float4 a4 = *(const float4 *)(e.sa + (EDGE ? min(i0 + 4 * chunk, m - 4) : i0 + 4 * chunk));
                 as[0] = e.alpha * a4.x; as[1] = e.alpha * a4.y; as[2] = e.alpha * a4.z; as[3] = e.alpha * a4.w;
               } else {
                 as[0] = as[1] = as[2] = as[3] = sa1;
@@ -546,34 +600,71 @@ __device__ __forceinline__ float edge_epilogue(const TileArgs &t, const Epilogue
 }
 
 
+// The epilogue of a 256 x 128 half tile (waves of 128 x 64: accumulator blocks y < 2): the whole tile in
+// FP32 is the ring, column c at buffer c / 16 as in edge_epilogue, written out once with bounds checks.
+__device__ __forceinline__ float half_tile_epilogue(const TileArgs &t, const Epilogue &e, v16f (&acc)[4][4], int i0,
+                                                    int j0, int wm, int wn, int lane, int tid, int vec) {
+  float mx = 0.f;
+  const EpiState st = epi_begin(e);
+  const int i = i0 + 4 * (tid & 63);  // this thread's 4 rows in the write-out
+  float rs[4], rb[4];                 // alpha * sa[i], bias[i] of those rows
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int iq = min(i + q, t.m - 1);
+    rs[q] = e.alpha * (e.sa_vec ? e.sa[iq] : scale_or_one(e.sa));
+    rb[q] = e.bias ? load_any(e.bias_dtype, e.bias, (size_t)iq, 1.f) : 0.f;
+  }
+  __syncthreads();  // the K loop no longer reads the ring
+#pragma unroll
+  for (int y = 0; y < 2; ++y) {
+    // column 64 wn + 32 y + lane % 32: buffer 4 wn + 2 y + (lane & 16 ? 1 : 0), column lane % 16 in it
+    float *grp = (lane & 16) ? stage_at(4 * wn + 2 * y + 1) : stage_at(4 * wn + 2 * y);
+    float *col = grp + (lane & 15) * kBM;
+#pragma unroll
+    for (int x = 0; x < 4; ++x)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int il = 128 * wm + 32 * x + 8 * g + 4 * (lane >> 5);
+        *(float4 *)(col + il) = make_float4(acc_read(acc[x][y][4 * g]), acc_read(acc[x][y][4 * g + 1]),
+                                            acc_read(acc[x][y][4 * g + 2]), acc_read(acc[x][y][4 * g + 3]));
+      }
+  }
+  __syncthreads();
+  return general_half<kAnyD, kAnyC>(e, st, t, i, j0, rs, rb, vec, tid, mx);
+}
+
 // Epilogue classes, one kernel instance each (kernels holding every epilogue spill registers, and the
-// spills cost the headline GEMM 4.6%): kEpiFast16 -- every tile full, no bias, beta = 0, a 2-byte D with
-// 16-byte aligned columns (staged16); kEpiFull -- every tile full, 4-element aligned D (staged_general);
-// kEpiAny -- everything, edge tiles included.
+// spills cost the headline GEMM 4.6%): kEpiFast16 -- no bias, beta = 0, a 2-byte D with 16-byte aligned
+// columns, m % 8 == 0 (staged16); kEpiFull -- 4-element aligned D and C, m % 4 == 0 (staged_general); kEpiAny -- unaligned
+// D or C, or m % 4 != 0,
+// every tile through the half-tile write-out with bounds checks and run-time dtypes (edge_epilogue).  The
+// staged write-outs take edge tiles themselves (the bounds-checked path had cost an edge tile ~30 us,
+// and a round waits for its slowest tile: 8000^2 x 8192 took 555 us against 399 us for 8192^2).
 constexpr int kEpiFast16 = 0, kEpiFull = 1, kEpiAny = 2;
 
 // the class a launch takes (host side)
 inline int epilogue_class(int m, int n, const Epilogue &e, int simple, int vec) {
-  const bool all_full = m % kBM == 0 && n % kBN == 0;
+  (void)n;  // the staged write-outs take edge tiles too
   const bool two_byte = e.d_dtype == E5MA_BF16 || e.d_dtype == E5MA_FP16;
-  if (all_full && simple && two_byte && (uintptr_t)e.d % 16 == 0 && e.ldd % 8 == 0) return kEpiFast16;
+  if (simple && two_byte && (uintptr_t)e.d % 16 == 0 && e.ldd % 8 == 0 && m % 8 == 0) return kEpiFast16;
   const bool c_ok = e.beta == 0.f || ((uintptr_t)e.c % (4 * elem_bytes(e.c_dtype)) == 0 && e.ldc % 4 == 0);
-  return all_full && vec && c_ok ? kEpiFull : kEpiAny;
+  return vec && c_ok && m % 4 == 0 ? kEpiFull : kEpiAny;  // m % 4: a thread's 4 rows never straddle m
 }
 
 // staged_general for D / C dtypes chosen at run time (the common pairings have their own instances)
-__device__ __forceinline__ float staged_full(const Epilogue &e, v16f (&acc)[4][4], int i0, int j0, int wm, int wn,
-                                             int lane, int tid, float sa1, float sb1) {
+template <bool EDGE>
+__device__ __forceinline__ float staged_full(const Epilogue &e, v16f (&acc)[4][4], int i0, int j0, int m, int n, int wm,
+                                             int wn, int lane, int tid, float sa1, float sb1) {
   const int dt = e.d_dtype, c = e.beta != 0.f ? e.c_dtype : -1;
   if (dt == E5MA_FP32 && c == E5MA_FP32)
-    return staged_general<E5MA_FP32, E5MA_FP32>(e, acc, i0, j0, wm, wn, lane, tid, sa1, sb1);
+    return staged_general<E5MA_FP32, E5MA_FP32, EDGE>(e, acc, i0, j0, m, n, wm, wn, lane, tid, sa1, sb1);
   if (c == -1) {
-    if (dt == E5MA_FP32) return staged_general<E5MA_FP32, -1>(e, acc, i0, j0, wm, wn, lane, tid, sa1, sb1);
-    if (dt == E5MA_BF16) return staged_general<E5MA_BF16, -1>(e, acc, i0, j0, wm, wn, lane, tid, sa1, sb1);
-    if (dt == E5MA_E5M2) return staged_general<E5MA_E5M2, -1>(e, acc, i0, j0, wm, wn, lane, tid, sa1, sb1);
-    if (dt == E5MA_E4M3) return staged_general<E5MA_E4M3, -1>(e, acc, i0, j0, wm, wn, lane, tid, sa1, sb1);
+    if (dt == E5MA_FP32) return staged_general<E5MA_FP32, -1, EDGE>(e, acc, i0, j0, m, n, wm, wn, lane, tid, sa1, sb1);
+    if (dt == E5MA_BF16) return staged_general<E5MA_BF16, -1, EDGE>(e, acc, i0, j0, m, n, wm, wn, lane, tid, sa1, sb1);
+    if (dt == E5MA_E5M2) return staged_general<E5MA_E5M2, -1, EDGE>(e, acc, i0, j0, m, n, wm, wn, lane, tid, sa1, sb1);
+    if (dt == E5MA_E4M3) return staged_general<E5MA_E4M3, -1, EDGE>(e, acc, i0, j0, m, n, wm, wn, lane, tid, sa1, sb1);
   }
-  return staged_general<kAnyD, kAnyC>(e, acc, i0, j0, wm, wn, lane, tid, sa1, sb1);
+  return staged_general<kAnyD, kAnyC, EDGE>(e, acc, i0, j0, m, n, wm, wn, lane, tid, sa1, sb1);
 }
 
 // The epilogue of a block tile (acc: this wave's accumulators; i0, j0: the tile's origin; sa1 = alpha * sa
@@ -585,19 +676,16 @@ __device__ __forceinline__ float tile_epilogue(const TileArgs &t, const Epilogue
                                                float sb1) {
   // (a scheduling barrier keeps the compiler from hoisting epilogue work into the K loop's tail)
   __builtin_amdgcn_sched_barrier(0);
+  const bool full = i0 + kBM <= t.m && j0 + kBN <= t.n;  // block-uniform
   if constexpr (EPI == kEpiFast16) {
-    return e.d_dtype == E5MA_BF16 ? staged16<E5MA_BF16>(e, acc, i0, j0, wm, wn, lane, tid, sa1, sb1)
-                                  : staged16<E5MA_FP16>(e, acc, i0, j0, wm, wn, lane, tid, sa1, sb1);
+    // one form for full and edge tiles: its checks are one predicate per store (m % 8 == 0)
+    return e.d_dtype == E5MA_BF16 ? staged16<E5MA_BF16, true>(e, acc, i0, j0, t.m, t.n, wm, wn, lane, tid, sa1, sb1)
+                                  : staged16<E5MA_FP16, true>(e, acc, i0, j0, t.m, t.n, wm, wn, lane, tid, sa1, sb1);
   } else if constexpr (EPI == kEpiFull) {
-    return staged_full(e, acc, i0, j0, wm, wn, lane, tid, sa1, sb1);
+    if (full) return staged_full<false>(e, acc, i0, j0, t.m, t.n, wm, wn, lane, tid, sa1, sb1);
+    return staged_full<true>(e, acc, i0, j0, t.m, t.n, wm, wn, lane, tid, sa1, sb1);
   } else {
-    const bool full = i0 + kBM <= t.m && j0 + kBN <= t.n;
-    if (full && simple && (e.d_dtype == E5MA_BF16 || e.d_dtype == E5MA_FP16) && ((uintptr_t)e.d & 15) == 0 &&
-        (e.ldd & 7) == 0)
-      return e.d_dtype == E5MA_BF16 ? staged16<E5MA_BF16>(e, acc, i0, j0, wm, wn, lane, tid, sa1, sb1)
-                                    : staged16<E5MA_FP16>(e, acc, i0, j0, wm, wn, lane, tid, sa1, sb1);
-    const bool c_ok = e.beta == 0.f || ((uintptr_t)e.c % (4 * elem_bytes(e.c_dtype)) == 0 && e.ldc % 4 == 0);
-    if (full && vec && c_ok) return staged_full(e, acc, i0, j0, wm, wn, lane, tid, sa1, sb1);
+    (void)simple;
     return edge_epilogue(t, e, acc, i0, j0, wm, wn, lane, tid, vec);
   }
 }

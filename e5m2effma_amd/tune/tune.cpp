@@ -8,7 +8,7 @@
 // candidate's on varied inputs; one that differs is reported and never picked.
 //
 //   e5ma_tune [header] [--dry-run]       tune, print the entry, and (unless --dry-run) rewrite header
-//   e5ma_tune --emit header arch cus splitk_div cast_grid adam_grid_bf16 adam_grid_fp32 quant_grid [name]
+//   e5ma_tune --emit header arch cus splitk_div cast_grid adam_grid_bf16 adam_grid_fp32 quant_grid tail_half [name]
 //                                        rewrite header with that entry, no device use (tests)
 //   e5ma_tune --ceiling                  AdamW over 2^28 parameters beside a kernel with the same memory
 //                                        accesses and no arithmetic (the access pattern's own ceiling)
@@ -20,6 +20,9 @@
 //   adam_grid_*     AdamW over 2^28 parameters, BF16 resp. FP32 state, with an E5M2 copy
 //   splitk_div      E5M2 x E5M2 -> BF16 TN GEMMs with at most 64 tiles: 512^2, 1024^2, 2048^2, 4096 x 1024
 //                   and 8192 x 64, all with k = 8192 (summed), given a full workspace (e5ma_gemm_ex)
+//   tail_half       0 / 1: TE wgrad (N, T) 14336 x 4096 x 8192 into FP32 with beta = 1 (896 tiles: a half-full
+//                   last round) and a half-filled grid, E5M2 x E4M3 -> BF16 TN 4096 x 2048 x 8192 (summed);
+//                   the candidates' outputs are compared bit for bit (half tiles must not change results)
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdio.h>
@@ -92,6 +95,22 @@ static std::vector<uint8_t> fetch(const void *p, size_t bytes) {
   std::vector<uint8_t> h(bytes);
   check(hipMemcpy(h.data(), p, bytes, hipMemcpyDeviceToHost), "hipMemcpy");
   return h;
+}
+
+// finite FP8 codes of moderate magnitude (exponent fields 12..19 for E5M2, 4..9 for E4M3), from a hash of i
+__global__ void fill_codes_kernel(uint8_t *p, size_t n, uint32_t seed, int fmt) {
+  for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+    uint32_t x = (uint32_t)i * 2654435761u ^ seed;
+    x ^= x >> 13;
+    x *= 0x5bd1e995u;
+    x ^= x >> 15;
+    p[i] = fmt == E5MA_E5M2 ? (uint8_t)((x & 0x83) | (((x >> 8) % 8 + 12) << 2))
+                            : (uint8_t)((x & 0x87) | (((x >> 8) % 6 + 4) << 3));
+  }
+}
+static void fill_codes(uint8_t *p, size_t n, uint32_t seed, int fmt) {
+  fill_codes_kernel<<<4096, 256>>>(p, n, seed, fmt);
+  check(hipGetLastError(), "fill_codes_kernel");
 }
 
 // AdamW's memory accesses without its arithmetic: per thread and step 8 elements of g, p, m and v read
@@ -286,7 +305,60 @@ static Tuning tune_device(const DeviceInfo &di) {
     t.splitk_div = pick("splitk_div", cands, ms, def.splitk_div);
     for (void *b : {(void *)A, (void *)B, D, ws.ptr}) check(hipFree(b), "hipFree");
   }
-  printf("outputs of %d cast / quantize candidates compared with their first candidate's: %d differ\n", checked,
+  // ---- half tiles for a half-full last round (results must not change) ----
+  {
+    struct Shape { int at, bt; bool akc, bkc; int m, n, k; int dt; float beta; };
+    const Shape shapes[] = {{E5MA_E5M2, E5MA_E4M3, false, false, 14336, 4096, 8192, E5MA_FP32, 1.f},
+                            {E5MA_E5M2, E5MA_E4M3, true, true, 4096, 2048, 8192, E5MA_BF16, 0.f}};
+    const size_t big = (size_t)14336 * 8192;
+    uint8_t *A = (uint8_t *)dalloc(big, 0), *B = (uint8_t *)dalloc(big, 0);
+    fill_codes(A, big, 11, E5MA_E5M2);
+    fill_codes(B, big, 12, E5MA_E4M3);
+    void *D = dalloc((size_t)14336 * 4096 * 4, 0);
+    const std::vector<int> cands = {0, 1};
+    std::vector<float> ms(cands.size(), 0.f);
+    std::vector<bool> ok(cands.size(), true);
+    for (const Shape &sh : shapes) {
+      std::vector<uint8_t> first;
+      for (size_t c = 0; c < cands.size(); ++c) {
+        DeviceInfo x = di;
+        x.tune = def;
+        x.tune.tail_half = cands[c];
+        dev::Epilogue e{};
+        e.alpha = 1.f;
+        e.beta = sh.beta;
+        e.c = sh.beta != 0.f ? D : nullptr;
+        e.ldc = sh.beta != 0.f ? sh.m : 0;
+        e.c_dtype = sh.dt;
+        e.d = D;
+        e.ldd = sh.m;
+        e.d_dtype = sh.dt;
+        e.bias_dtype = E5MA_FP32;
+        const long long lda = sh.akc ? sh.k : sh.m, ldb = sh.bkc ? sh.k : sh.n;
+        auto run = [&](int) {
+          return launch_gemm(sh.at, sh.bt, sh.akc, sh.bkc, A, lda, B, ldb, sh.m, sh.n, sh.k, e, x, Workspace{}, nullptr);
+        };
+        // one call from a zeroed D, compared bit for bit with the first candidate's
+        const size_t dbytes = (size_t)sh.m * sh.n * elem_bytes(sh.dt);
+        check(hipMemset(D, 0, dbytes), "hipMemset");
+        check(run(0), "launch");
+        check(hipDeviceSynchronize(), "hipDeviceSynchronize");
+        std::vector<uint8_t> got = fetch(D, dbytes);
+        if (c == 0) first = got;
+        else if (got != first) ok[c] = false;
+        ms[c] += best_ms(run, 5);
+      }
+    }
+    printf("FP8 GEMM half tiles for a half-full last round: TE wgrad 14336 x 4096 x 8192 (N, T, FP32, beta = 1) + "
+           "4096 x 2048 x 8192 TN (summed)\n");
+    t.tail_half = pick("tail_half", cands, ms, def.tail_half, ok);
+    for (size_t c = 1; c < cands.size(); ++c) {
+      ++checked;
+      if (!ok[c]) ++differing;
+    }
+    for (void *b : {(void *)A, (void *)B, D}) check(hipFree(b), "hipFree");
+  }
+  printf("outputs of %d cast / quantize / half-tile candidates compared with their first candidate's: %d differ\n", checked,
          differing);
   return t;
 }
@@ -307,8 +379,8 @@ static int emit(const char *path, const char *arch, int cus, const Tuning &t, co
     }
   }
   char buf[512];
-  snprintf(buf, sizeof buf, "  {\"%s\", %d, {%d, %d, %d, %d, %d}}, /* entry arch=%s cus=%d tuned on %s */ \\", arch, cus,
-           t.splitk_div, t.cast_grid, t.adam_grid_bf16, t.adam_grid_fp32, t.quant_grid, arch, cus, name);
+  snprintf(buf, sizeof buf, "  {\"%s\", %d, {%d, %d, %d, %d, %d, %d}}, /* entry arch=%s cus=%d tuned on %s */ \\", arch,
+           cus, t.splitk_div, t.cast_grid, t.adam_grid_bf16, t.adam_grid_fp32, t.quant_grid, t.tail_half, arch, cus, name);
   keep.push_back(buf);
   std::ofstream out(path);
   if (!out) {
@@ -317,7 +389,7 @@ static int emit(const char *path, const char *arch, int cus, const Tuning &t, co
   }
   out << "// e5ma_tuned.h -- written by the tuner (e5m2effma_amd/tune/tune.cpp; make -C e5m2effma_amd/csrc tune-run):\n"
          "// per-device launch choices of struct Tuning (e5ma_host.hpp), one entry per (architecture, CU count):\n"
-         "// {arch, cus, {splitk_div, cast_grid, adam_grid_bf16, adam_grid_fp32, quant_grid}}.  Re-running the\n"
+         "// {arch, cus, {splitk_div, cast_grid, adam_grid_bf16, adam_grid_fp32, quant_grid, tail_half}}.  Re-running the\n"
          "// tuner on a device adds or replaces that device's entry and keeps the others.\n"
          "#pragma once\n#define E5MA_TUNED_ENTRIES \\\n";
   for (const std::string &l : keep) out << l << "\n";
@@ -327,14 +399,15 @@ static int emit(const char *path, const char *arch, int cus, const Tuning &t, co
 }
 
 int main(int argc, char **argv) {
-  if (argc >= 10 && strcmp(argv[1], "--emit") == 0) {
+  if (argc >= 11 && strcmp(argv[1], "--emit") == 0) {
     Tuning t;
     t.splitk_div = atoi(argv[5]);
     t.cast_grid = atoi(argv[6]);
     t.adam_grid_bf16 = atoi(argv[7]);
     t.adam_grid_fp32 = atoi(argv[8]);
     t.quant_grid = atoi(argv[9]);
-    return emit(argv[2], argv[3], atoi(argv[4]), t, argc > 10 ? argv[10] : "unnamed device");
+    t.tail_half = atoi(argv[10]);
+    return emit(argv[2], argv[3], atoi(argv[4]), t, argc > 11 ? argv[11] : "unnamed device");
   }
   const char *path = "e5m2effma_amd/csrc/e5ma_tuned.h";
   bool dry = false, ceil_only = false;
@@ -366,7 +439,7 @@ int main(int argc, char **argv) {
   }
   printf("tuning on %s (%s, %d CUs)\n", name, arch, di.cus);
   const Tuning t = tune_device(di);
-  printf("entry: {\"%s\", %d, {%d, %d, %d, %d, %d}}\n", arch, di.cus, t.splitk_div, t.cast_grid, t.adam_grid_bf16,
-         t.adam_grid_fp32, t.quant_grid);
+  printf("entry: {\"%s\", %d, {%d, %d, %d, %d, %d, %d}}\n", arch, di.cus, t.splitk_div, t.cast_grid, t.adam_grid_bf16,
+         t.adam_grid_fp32, t.quant_grid, t.tail_half);
   return dry ? 0 : emit(path, arch, di.cus, t, name);
 }
