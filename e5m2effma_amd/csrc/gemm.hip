@@ -67,7 +67,7 @@ __global__ __launch_bounds__(kReduceThreads) void splitk_reduce_kernel(const flo
 }
 
 typedef hipError_t (*FastLaunch)(int, int, bool, bool, const uint8_t *, long long, const uint8_t *, long long, int, int,
-                                 int, int, int, const Epilogue &, hipStream_t);
+                                 int, int, int, int, const Epilogue &, hipStream_t);
 
 hipError_t launch_fast(FastLaunch launch, int round, int at, int bt, bool akc, bool bkc, const uint8_t *A, long long lda,
                        const uint8_t *B, long long ldb, int m, int n, int k, const Epilogue &e, const DeviceInfo &di,
@@ -75,8 +75,7 @@ hipError_t launch_fast(FastLaunch launch, int round, int at, int bt, bool akc, b
   const size_t cap = ws.ptr ? std::min(ws.bytes, kMaxWorkspace) : 0;
   const int splits = split_count(m, n, k, round, di.cus > 0 ? di.cus : 256, di.tune.splitk_div, cap);
   if (splits == 1) {
-    const int tail_cus = di.tune.tail_half && di.cus > 0 ? di.cus : 0;
-    return launch(at, bt, akc, bkc, A, lda, B, ldb, m, n, k, 1, tail_cus, e, s);
+    return launch(at, bt, akc, bkc, A, lda, B, ldb, m, n, k, 1, di.cus, di.tune.tail_half, e, s);
   }
   const long long ldw = partial_ld(m);
   Epilogue part{};  // raw FP32 partials: alpha 1, no scales, bias, C or amax
@@ -86,7 +85,7 @@ hipError_t launch_fast(FastLaunch launch, int round, int at, int bt, bool akc, b
   part.d_dtype = E5MA_FP32;
   part.c_dtype = E5MA_FP32;
   part.bias_dtype = E5MA_FP32;
-  hipError_t err = launch(at, bt, akc, bkc, A, lda, B, ldb, m, n, k, splits, 0, part, s);
+  hipError_t err = launch(at, bt, akc, bkc, A, lda, B, ldb, m, n, k, splits, di.cus, 0, part, s);
   if (err != hipSuccess) return err;
   const long long total = (m + 3) / 4 * (long long)n;
   const int grid = (int)std::min<long long>((total + kReduceThreads - 1) / kReduceThreads, 8192);

@@ -119,16 +119,17 @@ constexpr long long kMaxLd = 1LL << 24;
 // fast FP8 x FP8 path (gemm_f8.hip), any operand layout; akc / bkc: A / B K-contiguous
 bool gemm_f8_applies(int at, int bt, bool akc, bool bkc, int m, int n, int k, long long lda, long long ldb);
 hipError_t launch_gemm_f8(int at, int bt, bool akc, bool bkc, const uint8_t *A, long long lda, const uint8_t *B,
-                          long long ldb, int m, int n, int k, int splits, int tail_cus, const dev::Epilogue &e,
+                          long long ldb, int m, int n, int k, int splits, int cus, int tail_half, const dev::Epilogue &e,
                           hipStream_t s);
 // its instances, one translation unit per layout pair, named for (transa, transb):
 // tn = both K-contiguous, nn = A M-contiguous, nt = both M / N-contiguous, tt = B N-contiguous.
 // splits > 1: k is split into that many equal parts (each a multiple of the kernel's ring round), and
-// e describes FP32 partial outputs, split s at e.d + s * e.ldd * n floats.  tail_cus > 0 (FP8 kernel,
-// splits = 1): a last round of tiles at most half of tail_cus runs as half tiles (same results)
+// e describes FP32 partial outputs, split s at e.d + s * e.ldd * n floats.  FP8 kernel: cus > 0 caps the
+// grid at that many blocks, each taking every cus-th tile (persistent); tail_half (splits = 1): a last round
+// of at most cus / 2 tiles runs as half tiles.  The results are the same bits either way.
 #define E5MA_F8_LAYOUT_DECL(NAME)                                                                                   \
   hipError_t NAME(int at, int bt, const uint8_t *A, long long lda, const uint8_t *B, long long ldb, int m, int n, \
-                  int k, int splits, int tail_cus, const dev::Epilogue &e, hipStream_t s)
+                  int k, int splits, int cus, int tail_half, const dev::Epilogue &e, hipStream_t s)
 E5MA_F8_LAYOUT_DECL(launch_gemm_f8_tn);
 E5MA_F8_LAYOUT_DECL(launch_gemm_f8_nn);
 E5MA_F8_LAYOUT_DECL(launch_gemm_f8_nt);
@@ -136,7 +137,7 @@ E5MA_F8_LAYOUT_DECL(launch_gemm_f8_tt);
 // fast BF16-matrix-core path (gemm_h.hip): FP8 A x FP8 B (k < kF8MinK) or x K-contiguous BF16 B
 bool gemm_h_applies(int at, int bt, bool akc, bool bkc, int m, int n, int k);
 hipError_t launch_gemm_h(int at, int bt, bool akc, bool bkc, const uint8_t *A, long long lda, const uint8_t *B,
-                         long long ldb, int m, int n, int k, int splits, int tail_cus, const dev::Epilogue &e,
+                         long long ldb, int m, int n, int k, int splits, int cus, int tail_half, const dev::Epilogue &e,
                          hipStream_t s);
 // K of one ring round of the fast kernels (a split's K is a multiple of it, at least two of them)
 int gemm_f8_round();

@@ -17,10 +17,10 @@ bool gemm_f8_applies(int at, int bt, bool akc, bool bkc, int m, int n, int k, lo
 }
 
 hipError_t launch_gemm_f8(int at, int bt, bool akc, bool bkc, const uint8_t *A, long long lda, const uint8_t *B,
-                          long long ldb, int m, int n, int k, int splits, int tail_cus, const dev::Epilogue &e,
+                          long long ldb, int m, int n, int k, int splits, int cus, int tail_half, const dev::Epilogue &e,
                           hipStream_t s) {
-  if (akc) return (bkc ? launch_gemm_f8_tn : launch_gemm_f8_tt)(at, bt, A, lda, B, ldb, m, n, k, splits, tail_cus, e, s);
-  return (bkc ? launch_gemm_f8_nn : launch_gemm_f8_nt)(at, bt, A, lda, B, ldb, m, n, k, splits, tail_cus, e, s);
+  if (akc) return (bkc ? launch_gemm_f8_tn : launch_gemm_f8_tt)(at, bt, A, lda, B, ldb, m, n, k, splits, cus, tail_half, e, s);
+  return (bkc ? launch_gemm_f8_nn : launch_gemm_f8_nt)(at, bt, A, lda, B, ldb, m, n, k, splits, cus, tail_half, e, s);
 }
 
 int gemm_f8_round() { return kRound; }

@@ -2,5 +2,5 @@
 #include "gemm_f8_kernel.hpp"
 
 namespace e5ma {
-E5MA_F8_LAYOUT_DECL(launch_gemm_f8_tt) { return f8k::launch_layout<true, false>(at, bt, A, lda, B, ldb, m, n, k, splits, tail_cus, e, s); }
+E5MA_F8_LAYOUT_DECL(launch_gemm_f8_tt) { return f8k::launch_layout<true, false>(at, bt, A, lda, B, ldb, m, n, k, splits, cus, tail_half, e, s); }
 }  // namespace e5ma
