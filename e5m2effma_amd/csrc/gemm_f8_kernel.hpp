@@ -157,7 +157,7 @@ template <bool KC, bool PAIR, int J> __device__ __forceinline__ v8i read_frag(co
 
 // One unit: 4 NY MFMAs on fragment set P (NY = 4: a wave owns 128 x 128 of a 256 x 256 tile; NY = 2:
 // 128 x 64 of a 256 x 128 half tile, accumulator blocks y < 2).
-// BAR: starts with wait_barrier<WAITN, LGK>.
+// BAR: wait_barrier<WAITN, LGK> after the first MFMA, before any LDS read or load of the unit.
 // NEXT: the next unit's fragments (ring slot NS, unit NJ of that stage) are read into set 1 - P in the
 //   order its MFMAs use them (its first NY need a0 and all of b): a0, b0 .. b(NY - 1), a1, a2, a3, one
 //   every second MFMA (NY = 4) or every MFMA (NY = 2).
@@ -172,7 +172,6 @@ __device__ __forceinline__ void f8_unit(const Loads<PAIR> &L, int ls, int lane, 
   constexpr int Q = 1 - P, kMf = 4 * NY, kEvery = kMf / G::kLoads, kAt = kEvery > 1 ? 1 : 0;
   constexpr int kFragStep = NY == 4 ? 2 : 1;  // MFMAs per fragment read
   static_assert(kMf % G::kLoads == 0, "whole loads per unit");
-  if constexpr (BAR) wait_barrier<WAITN, LGK>();
   const uint8_t *na = G::template slot_a<NS>(), *nb = G::template slot_b<NS>();
 #pragma unroll
   for (int x = 0; x < 4; ++x) {
@@ -183,6 +182,15 @@ __device__ __forceinline__ void f8_unit(const Loads<PAIR> &L, int ls, int lane, 
       acc[x][y] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a[P][x], b[P][y], acc[x][y], kMfmaFmt<AT>,
                                                                   kMfmaFmt<BT>, 0, 0, 0, 0);
       const int i = NY * x + y;
+      if constexpr (BAR) {
+        // the unit's barrier comes after its first MFMA (whose fragments were read before it), so that the
+        // matrix core works through the wait; every LDS read and load of the unit follows it
+        if (i == 0) {
+          __builtin_amdgcn_sched_barrier(0);
+          wait_barrier<WAITN, LGK>();
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
       if constexpr (ISSUE) {
         if (i % kEvery == kAt) issue_load<IS, PAIR>(L, ls, i / kEvery);
       }

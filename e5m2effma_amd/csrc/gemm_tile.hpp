@@ -317,34 +317,84 @@ __device__ __forceinline__ uint32_t bf16_pair_canonical(uint32_t w) {
 // Set by any lane of the block whose converted values include a NaN (staged16)
 __shared__ int g_nan_flag;
 
-// Full tile, 2-byte output (BF16 / FP16), no bias, beta = 0.  sa1 = alpha * sa, sb1 = sb (per-tensor
-// values, read before the K loop); row / column scale vectors and amax are wave-uniform run-time choices.
-// Phase W: v = acc * ((alpha * sa[i]) * sb[j]) converted to DT; lanes l and l + 32 hold rows 8g..8g+3 and
-// 8g+4..8g+7 of one column, and one v_permlane32_swap per dword (which exchanges lanes 32..63 of its
+// BF16 output, no bias, beta = 0, no amax.  sa1 = alpha * sa, sb1 = sb (per-tensor values, read before
+// the K loop); VS: row / column scale vectors (either or both).  Each (EDGE, VS) pair is its own
+// straight-line copy: a copy with run-time flags held 256 VGPRs, spilled, and its scratch reload made
+// every tile wait for its own stores.
+// Phase W: v = acc * ((alpha * sa[i]) * sb[j]) converted to BF16; lanes l and l + 32 hold rows 8g..8g+3
+// and 8g+4..8g+7 of one column, and one v_permlane32_swap per dword (which exchanges lanes 32..63 of its
 // first operand with lanes 0..31 of its second) pairs groups 2p and 2p + 1 so that lane l holds rows
 // 16p..16p+7 and lane l + 32 rows 16p+8..16p+15: 16 bytes each, written to column j of the ring (512 bytes;
 // 32 columns per 16 KiB buffer) at 16-byte chunk k ^ (j % 16), so that the 16 lanes a ds_*_b128 serves per
-// cycle meet 16 distinct bank groups.  BF16 uses the hardware pair conversion, which keeps a NaN's sign and
-// payload: every lane folds 0 * v into a screen that is NaN exactly when some value is NaN or Inf, and a
-// block-wide flag then makes phase R rewrite NaN codes (rare path).
+// cycle meet 16 distinct bank groups.  The hardware pair conversion keeps a NaN's sign and payload: every
+// lane folds 0 * v into a screen that is NaN exactly when some value is NaN or Inf, and a block-wide flag
+// then makes phase R rewrite NaN codes to 0x7FC0 (rare path).
 // Phase R: step q writes tile columns 8q .. 8q + 7, thread t column 8q + t / 32, rows 8 (t % 32) .. + 7.
-// EDGE: the tile may reach past m or n (stores, scale reads and amax limited to D); false: a full tile,
-// no checks (the checks cost the 8192^3 GEMM 4 %).
-template <int DT, bool EDGE>
-__device__ __forceinline__ float staged16(const Epilogue &e, v16f (&acc)[4][4], int i0, int j0, int m, int n, int wm,
-                                          int wn, int lane, int tid, float sa1, float sb1) {
-  static_assert(elem_bytes(DT) == 2, "2-byte outputs");
-  float mx = 0.f;
+// Full tiles read the ring 8 steps at a time before their stores, so that the LDS latency is paid once per
+// 8 stores rather than once per store; edge tiles read per store (their reads sink into the store's
+// predicate).
+// EDGE: the tile may reach past m or n (stores and scale reads limited to D; m % 8 == 0, so a thread's 8
+// rows lie all inside or all outside D).
+template <bool EDGE, bool FIX>
+__device__ __forceinline__ void staged16_out(const Epilogue &e, int i0, int j0, int m, int n, int tid) {
+  constexpr int kBatch = EDGE ? 1 : 8;
+  const int cq = tid >> 5, k = tid & 31;
+  const bool rowv = i0 + 8 * k < m;
+  uint8_t *gp = (uint8_t *)e.d + ((size_t)(j0 + cq) * e.ldd + i0 + 8 * k) * 2;
+  const size_t gstep = (size_t)16 * e.ldd;  // 8 columns
+#pragma unroll
+  for (int q0 = 0; q0 < 32; q0 += kBatch) {
+    uint4 d[kBatch];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int q = q0 + u, cl = 8 * (q & 3) + cq;  // column within ring buffer q / 4
+      d[u] = *(const uint4 *)((const uint8_t *)stage_at(q >> 2) + cl * 512 + ((k ^ (cl & 15)) << 4));
+    }
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int q = q0 + u;
+      if constexpr (FIX) {
+        d[u].x = bf16_pair_canonical(d[u].x); d[u].y = bf16_pair_canonical(d[u].y);
+        d[u].z = bf16_pair_canonical(d[u].z); d[u].w = bf16_pair_canonical(d[u].w);
+      }
+      if (!EDGE || (rowv && j0 + 8 * q + cq < n)) *(uint4 *)(gp + q * gstep) = d[u];
+    }
+  }
+}
+
+template <bool EDGE, bool VS>
+__device__ __forceinline__ void staged16(const Epilogue &e, v16f (&acc)[4][4], int i0, int j0, int m, int n, int wm,
+                                         int wn, int lane, int tid, float sa1, float sb1) {
   const float s = sa1 * sb1;
-  const bool vs = e.sa_vec || e.sb_vec, amax = e.amax != nullptr;  // wave-uniform
   const int lc = lane & 31, hi = lane >> 5;
   float screen[2] = {0.f, 0.f};
+  // VS: this lane's 4 column scales and 16 row-group scales (alpha * sa[i]), loaded together
+  float sbv[4];
+  float4 sav[4][4];
+  if constexpr (VS) {
+#pragma unroll
+    for (int y = 0; y < 4; ++y) {
+      const int jc = j0 + 128 * wn + 32 * y + lc;  // past n (edge tiles) never stored
+      sbv[y] = e.sb_vec ? e.sb[EDGE ? min(jc, n - 1) : jc] : sb1;
+    }
+#pragma unroll
+    for (int x = 0; x < 4; ++x)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int r4 = i0 + 128 * wm + 32 * x + 8 * g + 4 * hi;  // rows r4 .. r4 + 3
+        if (e.sa_vec) {
+          // rows past m (edge tiles) read the last in-range group: never stored
+          const float4 a4 = *(const float4 *)(e.sa + (EDGE ? min(r4, m - 4) : r4));
+          sav[x][g] = make_float4(e.alpha * a4.x, e.alpha * a4.y, e.alpha * a4.z, e.alpha * a4.w);
+        } else {
+          sav[x][g] = make_float4(sa1, sa1, sa1, sa1);
+        }
+      }
+  }
   if (tid == 0) g_nan_flag = 0;
   __syncthreads();  // every wave has read its last fragments from the ring
 #pragma unroll
   for (int y = 0; y < 4; ++y) {
-    const int jc = j0 + 128 * wn + 32 * y + lc;  // this lane's column; past n (edge tiles) it is never stored
-    const float sbj = e.sb_vec ? e.sb[EDGE ? min(jc, n - 1) : jc] : sb1;
     uint8_t *col = (uint8_t *)stage_at(4 * wn + y) + lc * 512;
 #pragma unroll
     for (int x = 0; x < 4; ++x)
@@ -355,40 +405,20 @@ __device__ __forceinline__ float staged16(const Epilogue &e, v16f (&acc)[4][4], 
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
           const int g = 2 * p + h;
-          const int r4 = i0 + 128 * wm + 32 * x + 8 * g + 4 * hi;  // rows r4 .. r4 + 3
           float v[4];
-          if (vs) {
-            float as[4];
-            if (e.sa_vec) {
-              // rows past m (edge tiles; m % 8 == 0) read the last in-range group: never stored
-              const float4 a4 = *(const float4 *)(e.sa + (EDGE ? min(r4, m - 4) : r4));
-              as[0] = e.alpha * a4.x; as[1] = e.alpha * a4.y; as[2] = e.alpha * a4.z; as[3] = e.alpha * a4.w;
-            } else {
-              as[0] = as[1] = as[2] = as[3] = sa1;
-            }
+          if constexpr (VS) {
+            const float as[4] = {sav[x][g].x, sav[x][g].y, sav[x][g].z, sav[x][g].w};
 #pragma unroll
-            for (int q = 0; q < 4; ++q) v[q] = acc_read(acc[x][y][4 * g + q]) * (as[q] * sbj);
+            for (int q = 0; q < 4; ++q) v[q] = acc_read(acc[x][y][4 * g + q]) * (as[q] * sbv[y]);
           } else {
 #pragma unroll
             for (int q = 0; q < 4; ++q) v[q] = acc_read(acc[x][y][4 * g + q]) * s;
           }
-          if constexpr (DT == E5MA_BF16) {
 #pragma unroll
-            for (int q = 0; q < 4; ++q) screen[q & 1] = __builtin_fmaf(0.f, v[q], screen[q & 1]);
-          }
-          if (amax) {
-#pragma unroll
-            for (int q = 0; q < 4; ++q)
-              if (!EDGE || (jc < n && r4 + q < m)) mx = amax_fold(mx, v[q]);
-          }
-          if constexpr (DT == E5MA_BF16) {
-            typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-            w[2 * h] = __builtin_bit_cast(uint32_t, bf16x2_t{(__bf16)v[0], (__bf16)v[1]});
-            w[2 * h + 1] = __builtin_bit_cast(uint32_t, bf16x2_t{(__bf16)v[2], (__bf16)v[3]});
-          } else {
-            w[2 * h] = encode_t<DT>(v[0], 1.f) | encode_t<DT>(v[1], 1.f) << 16;
-            w[2 * h + 1] = encode_t<DT>(v[2], 1.f) | encode_t<DT>(v[3], 1.f) << 16;
-          }
+          for (int q = 0; q < 4; ++q) screen[q & 1] = __builtin_fmaf(0.f, v[q], screen[q & 1]);
+          typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+          w[2 * h] = __builtin_bit_cast(uint32_t, bf16x2_t{(__bf16)v[0], (__bf16)v[1]});
+          w[2 * h + 1] = __builtin_bit_cast(uint32_t, bf16x2_t{(__bf16)v[2], (__bf16)v[3]});
         }
         // (w0, w1): rows 8(2p) + 4 hi .. + 3; (w2, w3): rows 8(2p + 1) + 4 hi .. + 3
         const auto s0 = __builtin_amdgcn_permlane32_swap(w[0], w[2], false, false);
@@ -397,26 +427,10 @@ __device__ __forceinline__ float staged16(const Epilogue &e, v16f (&acc)[4][4], 
         *(uint4 *)(col + ((chunk ^ (lc & 15)) << 4)) = make_uint4(s0[0], s1[0], s0[1], s1[1]);
       }
   }
-  if constexpr (DT == E5MA_BF16) {
-    if (__builtin_isnan(screen[0] + screen[1])) g_nan_flag = 1;
-  }
+  if (__builtin_isnan(screen[0] + screen[1])) g_nan_flag = 1;
   __syncthreads();
-  const bool fix = DT == E5MA_BF16 && g_nan_flag != 0;
-  const int cq = tid >> 5, k = tid & 31;
-  const bool rowv = i0 + 8 * k < m;  // this thread's 8 rows: all below m or none (m % 8 == 0, class precondition)
-  uint8_t *gp = (uint8_t *)e.d + ((size_t)(j0 + cq) * e.ldd + i0 + 8 * k) * 2;
-  const size_t gstep = (size_t)16 * e.ldd;  // 8 columns
-#pragma unroll
-  for (int q = 0; q < 32; ++q) {
-    const int cl = 8 * (q & 3) + cq;  // column within ring buffer q / 4
-    uint4 d = *(const uint4 *)((const uint8_t *)stage_at(q >> 2) + cl * 512 + ((k ^ (cl & 15)) << 4));
-    if (fix) {
-      d.x = bf16_pair_canonical(d.x); d.y = bf16_pair_canonical(d.y);
-      d.z = bf16_pair_canonical(d.z); d.w = bf16_pair_canonical(d.w);
-    }
-    if (!EDGE || (rowv && j0 + 8 * q + cq < n)) *(uint4 *)(gp + q * gstep) = d;
-  }
-  return mx;
+  if (g_nan_flag != 0) staged16_out<EDGE, true>(e, i0, j0, m, n, tid);
+  else staged16_out<EDGE, false>(e, i0, j0, m, n, tid);
 }
 
 // Full tile, any output dtype, bias and beta * C (CT: C's dtype, -1 when beta = 0), 4-element aligned
@@ -634,9 +648,9 @@ __device__ __forceinline__ float half_tile_epilogue(const TileArgs &t, const Epi
 }
 
 // Epilogue classes, one kernel instance each (kernels holding every epilogue spill registers, and the
-// spills cost the headline GEMM 4.6%): kEpiFast16 -- no bias, beta = 0, a 2-byte D with 16-byte aligned
-// columns, m % 8 == 0 (staged16); kEpiFull -- 4-element aligned D and C, m % 4 == 0 (staged_general); kEpiAny -- unaligned
-// D or C, or m % 4 != 0,
+// spills cost the headline GEMM 4.6%): kEpiFast16 -- no bias, beta = 0, no amax, a BF16 D with 16-byte
+// aligned columns, m % 8 == 0 (staged16); kEpiFull -- 4-element aligned D and C, m % 4 == 0
+// (staged_general; FP16 D and amax too); kEpiAny -- unaligned D or C, or m % 4 != 0,
 // every tile through the half-tile write-out with bounds checks and run-time dtypes (edge_epilogue).  The
 // staged write-outs take edge tiles themselves (the bounds-checked path had cost an edge tile ~30 us,
 // and a round waits for its slowest tile: 8000^2 x 8192 took 555 us against 399 us for 8192^2).
@@ -645,8 +659,9 @@ constexpr int kEpiFast16 = 0, kEpiFull = 1, kEpiAny = 2;
 // the class a launch takes (host side)
 inline int epilogue_class(int m, int n, const Epilogue &e, int simple, int vec) {
   (void)n;  // the staged write-outs take edge tiles too
-  const bool two_byte = e.d_dtype == E5MA_BF16 || e.d_dtype == E5MA_FP16;
-  if (simple && two_byte && (uintptr_t)e.d % 16 == 0 && e.ldd % 8 == 0 && m % 8 == 0) return kEpiFast16;
+  if (simple && e.d_dtype == E5MA_BF16 && e.amax == nullptr && (uintptr_t)e.d % 16 == 0 && e.ldd % 8 == 0 &&
+      m % 8 == 0)
+    return kEpiFast16;
   const bool c_ok = e.beta == 0.f || ((uintptr_t)e.c % (4 * elem_bytes(e.c_dtype)) == 0 && e.ldc % 4 == 0);
   return vec && c_ok && m % 4 == 0 ? kEpiFull : kEpiAny;  // m % 4: a thread's 4 rows never straddle m
 }
@@ -678,9 +693,15 @@ __device__ __forceinline__ float tile_epilogue(const TileArgs &t, const Epilogue
   __builtin_amdgcn_sched_barrier(0);
   const bool full = i0 + kBM <= t.m && j0 + kBN <= t.n;  // block-uniform
   if constexpr (EPI == kEpiFast16) {
-    // one form for full and edge tiles: its checks are one predicate per store (m % 8 == 0)
-    return e.d_dtype == E5MA_BF16 ? staged16<E5MA_BF16, true>(e, acc, i0, j0, t.m, t.n, wm, wn, lane, tid, sa1, sb1)
-                                  : staged16<E5MA_FP16, true>(e, acc, i0, j0, t.m, t.n, wm, wn, lane, tid, sa1, sb1);
+    const bool vs = e.sa_vec || e.sb_vec;  // launch-uniform
+    if (full) {
+      if (vs) staged16<false, true>(e, acc, i0, j0, t.m, t.n, wm, wn, lane, tid, sa1, sb1);
+      else staged16<false, false>(e, acc, i0, j0, t.m, t.n, wm, wn, lane, tid, sa1, sb1);
+    } else {
+      if (vs) staged16<true, true>(e, acc, i0, j0, t.m, t.n, wm, wn, lane, tid, sa1, sb1);
+      else staged16<true, false>(e, acc, i0, j0, t.m, t.n, wm, wn, lane, tid, sa1, sb1);
+    }
+    return 0.f;  // no amax in this class
   } else if constexpr (EPI == kEpiFull) {
     if (full) return staged_full<false>(e, acc, i0, j0, t.m, t.n, wm, wn, lane, tid, sa1, sb1);
     return staged_full<true>(e, acc, i0, j0, t.m, t.n, wm, wn, lane, tid, sa1, sb1);
