@@ -161,11 +161,13 @@ template <bool KC, bool PAIR, int J> __device__ __forceinline__ v8i read_frag(co
 // NEXT: the next unit's fragments (ring slot NS, unit NJ of that stage) are read into set 1 - P in the
 //   order its MFMAs use them (its first NY need a0 and all of b): a0, b0 .. b(NY - 1), a1, a2, a3, one
 //   every second MFMA (NY = 4) or every MFMA (NY = 2).
+// ZERO: the tile's first unit, whose MFMAs take the inline constant 0 as their accumulator input (no
+//   zeroing of 256 accumulator registers per tile).
 // ISSUE: stage ls's loads go into ring slot IS, one pair (A, B) after every (4 NY / kLoads)-th MFMA.  A
 //   half tile issues every load of a whole tile (the B rows it does not use included), so that every
 //   wait count is the same for both widths.
 template <bool PAIR, int P, bool BAR, int WAITN, int LGK, bool NEXT, int NS, int NJ, bool ISSUE, int IS, int AT,
-          int BT, bool AKC, bool BKC, int NY>
+          int BT, bool AKC, bool BKC, int NY, bool ZERO = false>
 __device__ __forceinline__ void f8_unit(const Loads<PAIR> &L, int ls, int lane, int wm, int wn, v8i (&a)[2][4],
                                         v8i (&b)[2][4], v16f (&acc)[4][4]) {
   using G = Ring<PAIR>;
@@ -179,8 +181,8 @@ __device__ __forceinline__ void f8_unit(const Loads<PAIR> &L, int ls, int lane, 
     for (int y = 0; y < NY; ++y) {
       // scale operands 0 select the unscaled v_mfma_f32_32x32x64_f8f6f4 (same products as the scaled form
       // with the neutral scale 127, one instruction dword pair shorter)
-      acc[x][y] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a[P][x], b[P][y], acc[x][y], kMfmaFmt<AT>,
-                                                                  kMfmaFmt<BT>, 0, 0, 0, 0);
+      acc[x][y] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a[P][x], b[P][y], ZERO ? v16f{} : acc[x][y],
+                                                                  kMfmaFmt<AT>, kMfmaFmt<BT>, 0, 0, 0, 0);
       const int i = NY * x + y;
       if constexpr (BAR) {
         // the unit's barrier comes after its first MFMA (whose fragments were read before it), so that the
@@ -239,7 +241,12 @@ __device__ __forceinline__ void k_loop(const Loads<false> &L, int nk, int lane, 
   }
   // four stages per iteration, each awaiting s + 1 (s + 2 in flight) and issuing s + 3; then the last
   // four drain the ring (nk % 4 == 0, nk >= 8)
-  int s = 0;
+  // the first iteration, peeled: its first unit starts the accumulators (nk >= 8)
+  f8_unit<false, 0, true, W, kLgk, true, 1, 0, true, 3, AT, BT, AKC, BKC, NY, true>(L, 3, lane, wm, wn, a, b, acc);
+  f8_unit<false, 1, true, W, kLgk, true, 2, 0, true, 0, AT, BT, AKC, BKC, NY>(L, 4, lane, wm, wn, a, b, acc);
+  f8_unit<false, 0, true, W, kLgk, true, 3, 0, true, 1, AT, BT, AKC, BKC, NY>(L, 5, lane, wm, wn, a, b, acc);
+  f8_unit<false, 1, true, W, kLgk, true, 0, 0, true, 2, AT, BT, AKC, BKC, NY>(L, 6, lane, wm, wn, a, b, acc);
+  int s = 4;
   for (; s < nk - 4; s += 4) {
     f8_unit<false, 0, true, W, kLgk, true, 1, 0, true, 3, AT, BT, AKC, BKC, NY>(L, s + 3, lane, wm, wn, a, b, acc);
     f8_unit<false, 1, true, W, kLgk, true, 2, 0, true, 0, AT, BT, AKC, BKC, NY>(L, s + 4, lane, wm, wn, a, b, acc);
@@ -269,7 +276,12 @@ __device__ __forceinline__ void k_loop(const Loads<true> &L, int nk, int lane, i
   }
   // two stages (one per region) per iteration, each issuing stage p + 2 in its second unit; then the
   // last two stages
-  int p = 0;
+  // the first iteration, peeled: its first unit starts the accumulators (np >= 4)
+  f8_unit<true, 0, false, 0, 0, true, 0, 1, false, 0, AT, BT, AKC, BKC, NY, true>(L, 0, lane, wm, wn, a, b, acc);
+  f8_unit<true, 1, true, 0, 0, true, 1, 0, true, 0, AT, BT, AKC, BKC, NY>(L, 2, lane, wm, wn, a, b, acc);
+  f8_unit<true, 0, false, 0, 0, true, 1, 1, false, 0, AT, BT, AKC, BKC, NY>(L, 0, lane, wm, wn, a, b, acc);
+  f8_unit<true, 1, true, 0, 0, true, 0, 0, true, 1, AT, BT, AKC, BKC, NY>(L, 3, lane, wm, wn, a, b, acc);
+  int p = 2;
   for (; p < np - 2; p += 2) {
     f8_unit<true, 0, false, 0, 0, true, 0, 1, false, 0, AT, BT, AKC, BKC, NY>(L, 0, lane, wm, wn, a, b, acc);
     f8_unit<true, 1, true, 0, 0, true, 1, 0, true, 0, AT, BT, AKC, BKC, NY>(L, p + 2, lane, wm, wn, a, b, acc);
@@ -306,13 +318,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_f8_kernel(TileArgs t0, Epilo
     apply_split(t, e, sp);
     const int i0 = tm * kBM, j0 = tn * kBN;
 
-    v16f acc[4][4];
-#pragma unroll
-    for (int x = 0; x < 4; ++x)
-#pragma unroll
-      for (int y = 0; y < 4; ++y)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc[x][y][r] = 0.f;
+    v16f acc[4][4];          // started by the K loop's first unit
     v8i a[2][4], b[2][4];  // fragments, double-buffered by unit parity
     const Loads<PAIR> L = make_loads<AKC, BKC, PAIR>(t, i0, j0, wave, lane);
     k_loop<AT, BT, AKC, BKC, 4>(L, t.k / kUnitK, lane, wm, wn, a, b, acc);
@@ -338,13 +344,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_f8_half_kernel(TileArgs t, E
   const int i0 = tm * kBM, j0 = tn * kBN + 128 * h;
   if (j0 >= t.n) return;  // the right half of a tile narrower than 129 columns: nothing to do (whole block)
 
-  v16f acc[4][4];
-#pragma unroll
-  for (int x = 0; x < 4; ++x)
-#pragma unroll
-    for (int y = 0; y < 4; ++y)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[x][y][r] = 0.f;
+  v16f acc[4][4];  // blocks y < 2 started by the K loop's first unit; the others are not used
   v8i a[2][4], b[2][4];
   const Loads<PAIR> L = make_loads<AKC, BKC, PAIR>(t, i0, j0, wave, lane);
   k_loop<AT, BT, AKC, BKC, 2>(L, t.k / kUnitK, lane, wm, wn, a, b, acc);

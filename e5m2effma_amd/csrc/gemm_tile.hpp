@@ -327,8 +327,8 @@ __shared__ int g_nan_flag;
 // 16p..16p+7 and lane l + 32 rows 16p+8..16p+15: 16 bytes each, written to column j of the ring (512 bytes;
 // 32 columns per 16 KiB buffer) at 16-byte chunk k ^ (j % 16), so that the 16 lanes a ds_*_b128 serves per
 // cycle meet 16 distinct bank groups.  The hardware pair conversion keeps a NaN's sign and payload: every
-// lane folds 0 * v into a screen that is NaN exactly when some value is NaN or Inf, and a block-wide flag
-// then makes phase R rewrite NaN codes to 0x7FC0 (rare path).
+// lane folds 0 * v of the converted pairs into a screen that is NaN exactly when some value is NaN or Inf
+// (BF16 keeps both), and a block-wide flag then makes phase R rewrite NaN codes to 0x7FC0 (rare path).
 // Phase R: step q writes tile columns 8q .. 8q + 7, thread t column 8q + t / 32, rows 8 (t % 32) .. + 7.
 // Full tiles read the ring 8 steps at a time before their stores, so that the LDS latency is paid once per
 // 8 stores rather than once per store; edge tiles read per store (their reads sink into the store's
@@ -362,6 +362,8 @@ __device__ __forceinline__ void staged16_out(const Epilogue &e, int i0, int j0, 
   }
 }
 
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
 template <bool EDGE, bool VS>
 __device__ __forceinline__ void staged16(const Epilogue &e, v16f (&acc)[4][4], int i0, int j0, int m, int n, int wm,
                                          int wn, int lane, int tid, float sa1, float sb1) {
@@ -391,11 +393,18 @@ __device__ __forceinline__ void staged16(const Epilogue &e, v16f (&acc)[4][4], i
         }
       }
   }
+  // this lane's byte offsets in a column group for register groups (x, p): column lc's 512 bytes, 16-byte
+  // chunk (16 wm + 4 x + 2 p + hi) ^ (lc % 16)
+  uint32_t off[4][2];
+#pragma unroll
+  for (int x = 0; x < 4; ++x)
+#pragma unroll
+    for (int p = 0; p < 2; ++p) off[x][p] = lc * 512 + (((16 * wm + 4 * x + 2 * p + hi) ^ (lc & 15)) << 4);
   if (tid == 0) g_nan_flag = 0;
   __syncthreads();  // every wave has read its last fragments from the ring
 #pragma unroll
   for (int y = 0; y < 4; ++y) {
-    uint8_t *col = (uint8_t *)stage_at(4 * wn + y) + lc * 512;
+    uint8_t *col = (uint8_t *)stage_at(4 * wn + y);
 #pragma unroll
     for (int x = 0; x < 4; ++x)
 #pragma unroll
@@ -414,17 +423,18 @@ __device__ __forceinline__ void staged16(const Epilogue &e, v16f (&acc)[4][4], i
 #pragma unroll
             for (int q = 0; q < 4; ++q) v[q] = acc_read(acc[x][y][4 * g + q]) * s;
           }
-#pragma unroll
-          for (int q = 0; q < 4; ++q) screen[q & 1] = __builtin_fmaf(0.f, v[q], screen[q & 1]);
-          typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-          w[2 * h] = __builtin_bit_cast(uint32_t, bf16x2_t{(__bf16)v[0], (__bf16)v[1]});
-          w[2 * h + 1] = __builtin_bit_cast(uint32_t, bf16x2_t{(__bf16)v[2], (__bf16)v[3]});
+          const bf16x2 lo{(__bf16)v[0], (__bf16)v[1]}, hi2{(__bf16)v[2], (__bf16)v[3]};
+          // 0 * a + 0 * b + screen per BF16 pair: NaN exactly when a or b is NaN or Inf (one instruction for
+          // two values)
+          screen[0] = __builtin_amdgcn_fdot2_f32_bf16(lo, bf16x2{}, screen[0], false);
+          screen[1] = __builtin_amdgcn_fdot2_f32_bf16(hi2, bf16x2{}, screen[1], false);
+          w[2 * h] = __builtin_bit_cast(uint32_t, lo);
+          w[2 * h + 1] = __builtin_bit_cast(uint32_t, hi2);
         }
         // (w0, w1): rows 8(2p) + 4 hi .. + 3; (w2, w3): rows 8(2p + 1) + 4 hi .. + 3
         const auto s0 = __builtin_amdgcn_permlane32_swap(w[0], w[2], false, false);
         const auto s1 = __builtin_amdgcn_permlane32_swap(w[1], w[3], false, false);
-        const int chunk = 16 * wm + 4 * x + 2 * p + hi;
-        *(uint4 *)(col + ((chunk ^ (lc & 15)) << 4)) = make_uint4(s0[0], s1[0], s0[1], s1[1]);
+        *(uint4 *)(col + off[x][p]) = make_uint4(s0[0], s1[0], s0[1], s1[1]);
       }
   }
   if (__builtin_isnan(screen[0] + screen[1])) g_nan_flag = 1;

@@ -450,6 +450,35 @@ def test_direct_epilogue_bf16_nan_codes(dev):
     assert bad == 0, first
 
 
+@pytest.mark.parametrize("k", [8192, 1024])
+@pytest.mark.parametrize("m,n", [(2304, 2048), (2264, 2056)])
+@pytest.mark.parametrize("vec", [False, True])
+def test_staged16_bf16_nan_codes(dev, k, m, n, vec):
+    """The 2-byte write-out (BF16 D, no bias, beta = 0, no amax, ldd % 8 == 0, m % 8 == 0) in each of its
+    copies: full tiles (2304 x 2048) and edge tiles (2264 x 2056), per-tensor and per-row / per-column
+    scales, on the FP8 (k = 8192) and the BF16 (k = 1024) matrix cores.  NaN codes of A make rows 5 and 6
+    NaN, which must come out as 0x7FC0 (the screen over the converted pairs sets the block's flag); an Inf
+    code makes row 9 Inf or NaN; sampled outputs elsewhere against the oracle's bound."""
+    rng = np.random.default_rng(9950 + k + m + 3 * vec)
+    sa = (rng.uniform(0.5, 2.0, m).astype(np.float32) / 64) if vec else 1.0 / 64
+    sb = rng.uniform(0.5, 2.0, n).astype(np.float32) if vec else 0.5
+    case = gu.GemmCase(rng, 1, 0, m, n, k, E5, E4, ddt=B16, sa=sa, sb=sb, dist="normal", sigma=1.0, pad=0,
+                       ldd=m + 8)
+    A = case.A.copy()
+    A[5 * k + 7] = 0x7F   # NaN
+    A[6 * k + 3] = 0xFE   # negative NaN
+    A[9 * k + 1] = 0x7C   # +Inf
+    case.A = A
+    s, D, _ = case.run(dev)
+    assert s == 0, gu._lib.last_error()
+    Dm = D.view(np.uint16).reshape(n, case.ldd)[:, :m]
+    assert (Dm[:, 5] == 0x7FC0).all() and (Dm[:, 6] == 0x7FC0).all()
+    r9 = Dm[:, 9]
+    assert (((r9 & 0x7FFF) == 0x7F80) | (r9 == 0x7FC0)).all()
+    bad, first = case.check(D, samples=4096, rng=rng)
+    assert bad == 0, first
+
+
 # ---- the direct epilogue (full tiles, no bias, beta = 0, D columns 16-byte aligned: ldd % 4 == 0) on
 # unsplit grids (more than 64 tiles), every output dtype, outer scales, amax ---------------------------
 @pytest.mark.parametrize("ddt", [B16, F16, F32, E5, E4])
