@@ -443,6 +443,29 @@ __device__ __forceinline__ void staged16(const Epilogue &e, v16f (&acc)[4][4], i
   else staged16_out<EDGE, false>(e, i0, j0, m, n, tid);
 }
 
+typedef unsigned int v2u __attribute__((ext_vector_type(2)));
+
+// load4_t with non-temporal loads (C of the full-tile write-out: read once, kept out of the caches' way)
+template <int T> __device__ __forceinline__ void load4_nt(const void *p, size_t idx, float sinv, float (&o)[4]) {
+  const uint8_t *b = (const uint8_t *)p + idx * elem_bytes(T);
+  if constexpr (T == E5MA_FP32) {
+    const v4f v = __builtin_nontemporal_load((const v4f *)b);
+    o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
+  } else if constexpr (elem_bytes(T) == 2) {
+    const v2u v = __builtin_nontemporal_load((const v2u *)b);
+    const uint32_t h[4] = {v.x & 0xFFFFu, v.x >> 16, v.y & 0xFFFFu, v.y >> 16};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) o[q] = T == E5MA_BF16 ? bf16_value(h[q]) : f16_value(h[q]);
+  } else {
+    const uint32_t v = __builtin_nontemporal_load((const uint32_t *)b);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t c = (v >> (8 * q)) & 0xFFu;
+      o[q] = (T == E5MA_E5M2 ? e5m2_value(c) : e4m3_value(c)) * sinv;
+    }
+  }
+}
+
 // Full tile, any output dtype, bias and beta * C (CT: C's dtype, -1 when beta = 0), 4-element aligned
 // D and C: two passes, one per half of the tile's columns (128 columns x 256 rows of FP32,
 // the whole ring).
@@ -452,6 +475,9 @@ __device__ __forceinline__ void staged16(const Epilogue &e, v16f (&acc)[4][4], i
 // read and D written along whole columns; v = v + bias[i]; v = fma(beta, C * csinv, v); amax; convert
 // (the order of include/e5m2effma.h).  C is loaded a group of 8 steps ahead of its use, the next half's
 // first group before that half is staged (a load waited on right away left the TE wgrad GEMM 17% slower).
+// C is read and D written non-temporally: an FP32 C and D (TE wgrad's main_grad, 235 MB) otherwise pushed the
+// operands out of the Infinity Cache, and the K loops waited on HBM (wgrad 4096 x 14336 x 8192: 474 -> 419 us;
+// either one alone: 474 / 462 us).
 // C may alias D: each thread reads its own elements before it writes them, and no other thread writes them.
 template <int DT, int CT, bool EDGE>
 __device__ __forceinline__ float staged_general(const Epilogue &e, v16f (&acc)[4][4], int i0, int j0, int m, int n,
@@ -482,7 +508,7 @@ __device__ __forceinline__ float staged_general(const Epilogue &e, v16f (&acc)[4
       // C exists for these elements (edge tiles: not past m or n); 4-element aligned (class precondition)
       if ((!EDGE || (j < n && rowv)) && (CT != kAnyC || e.beta != 0.f)) {
         if constexpr (CT == kAnyC) load4_any(e.c_dtype, e.c, (size_t)j * e.ldc + i, csinv, c[u]);
-        else if constexpr (CT >= 0) load4_t<CT>(e.c, (size_t)j * e.ldc + i, csinv, c[u]);
+        else if constexpr (CT >= 0) load4_nt<CT>(e.c, (size_t)j * e.ldc + i, csinv, c[u]);
       }
     }
   };
@@ -525,13 +551,15 @@ __device__ __forceinline__ float staged_general(const Epilogue &e, v16f (&acc)[4
       } else {
         uint8_t *dp = (uint8_t *)e.d + ((size_t)j * e.ldd + i) * elem_bytes(DT);
         if constexpr (DT == E5MA_FP32) {
-          *(float4 *)dp = make_float4(v[0], v[1], v[2], v[3]);
+          __builtin_nontemporal_store(v4f{v[0], v[1], v[2], v[3]}, (v4f *)dp);
         } else if constexpr (is_fp8(DT)) {
-          *(uint32_t *)dp = encode_t<DT>(v[0], qs) | encode_t<DT>(v[1], qs) << 8 | encode_t<DT>(v[2], qs) << 16 |
-                            encode_t<DT>(v[3], qs) << 24;
+          __builtin_nontemporal_store(encode_t<DT>(v[0], qs) | encode_t<DT>(v[1], qs) << 8 |
+                                          encode_t<DT>(v[2], qs) << 16 | encode_t<DT>(v[3], qs) << 24,
+                                      (uint32_t *)dp);
         } else {
-          *(uint2 *)dp = make_uint2(encode_t<DT>(v[0], 1.f) | encode_t<DT>(v[1], 1.f) << 16,
-                                    encode_t<DT>(v[2], 1.f) | encode_t<DT>(v[3], 1.f) << 16);
+          __builtin_nontemporal_store(v2u{encode_t<DT>(v[0], 1.f) | encode_t<DT>(v[1], 1.f) << 16,
+                                          encode_t<DT>(v[2], 1.f) | encode_t<DT>(v[3], 1.f) << 16},
+                                      (v2u *)dp);
         }
       }
     }
