@@ -3,6 +3,8 @@
 // 128 KiB LDS ring of 8 buffers and its direct-to-LDS loads, the XCD-aware tile order, and the
 // epilogues, which stage the finished tile in the ring.
 #pragma once
+#include <type_traits>
+
 #include "e5ma_host.hpp"
 #include "gemm_common.hpp"
 
@@ -466,12 +468,18 @@ template <int T> __device__ __forceinline__ void load4_nt(const void *p, size_t 
   }
 }
 
+// Tile column of pass column pc (0..127) in pass h of staged_general: a pass takes 64 columns of each wave
+// column wn = pc / 64, i.e. tile columns 128 (pc / 64) + 64 h + pc % 64.
+__device__ __forceinline__ int pass_col(int h, int pc) { return 128 * (pc >> 6) + 64 * h + (pc & 63); }
+
 // Full tile, any output dtype, bias and beta * C (CT: C's dtype, -1 when beta = 0), 4-element aligned
-// D and C: two passes, one per half of the tile's columns (128 columns x 256 rows of FP32,
-// the whole ring).
-// Phase W: the two waves holding the half write v = acc * ((alpha * sa[i]) * sb[j]), 4 rows (16 bytes) per
-// lane and group, column c of the half at 1 KiB in buffer c / 16, 16-byte chunk k at k ^ (c % 16).
-// Phase R: thread t takes rows 4 (t % 64) .. + 3 of column 4q + t / 64 of the half (q = 0..31), so C is
+// D and C: two passes, each over half of the tile's columns (128 columns x 256 rows of FP32, the whole
+// ring): pass h takes accumulator blocks y = 2h, 2h + 1 of every wave, so all four waves stage in each
+// pass (with the halves of the tile per pass, two waves stood idle through each staging: 8.4K cycles
+// per pass in TE wgrad, against its 15K-cycle write-out).
+// Phase W: every wave writes v = acc * ((alpha * sa[i]) * sb[j]), 4 rows (16 bytes) per lane and group,
+// pass column c at 1 KiB in buffer c / 16, 16-byte chunk k at k ^ (c % 16).
+// Phase R: thread t takes rows 4 (t % 64) .. + 3 of pass column 4q + t / 64 (q = 0..31), so C is
 // read and D written along whole columns; v = v + bias[i]; v = fma(beta, C * csinv, v); amax; convert
 // (the order of include/e5m2effma.h).  C is loaded a group of 8 steps ahead of its use, the next half's
 // first group before that half is staged (a load waited on right away left the TE wgrad GEMM 17% slower).
@@ -502,7 +510,7 @@ __device__ __forceinline__ float staged_general(const Epilogue &e, v16f (&acc)[4
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       const int q = 8 * (g & 3) + u;
-      const int j = j0 + 128 * (g >> 2) + 4 * q + cq;
+      const int j = j0 + pass_col(g >> 2, 4 * q + cq);
 #pragma unroll
       for (int r = 0; r < 4; ++r) c[u][r] = 0.f;
       // C exists for these elements (edge tiles: not past m or n); 4-element aligned (class precondition)
@@ -523,7 +531,7 @@ __device__ __forceinline__ float staged_general(const Epilogue &e, v16f (&acc)[4
     for (int u = 0; u < 8; ++u) {
       const int q = 8 * gq + u;
       const int cl = 4 * (q & 3) + cq;  // column within ring buffer q / 4
-      const int j = j0 + 128 * h + 4 * q + cq;
+      const int j = j0 + pass_col(h, 4 * q + cq);
       const float4 x4 = *(const float4 *)(stage_at(q >> 2) + cl * 256 + ((kr ^ cl) << 2));
       float v[4] = {x4.x, x4.y, x4.z, x4.w};
 #pragma unroll
@@ -566,17 +574,21 @@ __device__ __forceinline__ float staged_general(const Epilogue &e, v16f (&acc)[4
     __builtin_amdgcn_sched_barrier(0);
   };
   if constexpr (CT != -1) load_group(0, ca);
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
+  // pass h (a compile-time constant: it selects accumulator blocks, which must not be indexed at run time)
+  auto pass = [&](auto hc) {
+    constexpr int h = decltype(hc)::value;
     __syncthreads();  // the ring is free: the K loop's fragments, or the previous half, have been read
-    if (wn == h) {
+    {
 #pragma unroll
-      for (int y = 0; y < 4; ++y) {
-        const int c = 32 * y + (lane & 31);  // column within the half
+      for (int yy = 0; yy < 2; ++yy) {
+        const int y = 2 * h + yy;
+        const int jt = 128 * wn + 32 * y + (lane & 31);  // tile column
         float sbj = sb1;
-        if (e.sb_vec) sbj = e.sb[EDGE ? min(j0 + 128 * h + c, n - 1) : j0 + 128 * h + c];  // past n: never stored
-        // buffer c / 16 = 2 y + (lane & 16 ? 1 : 0): a select between two pointers, not a lane-indexed switch
-        float *colp = ((lane & 16) ? stage_at(2 * y + 1) : stage_at(2 * y)) + lc * 256;
+        if (e.sb_vec) sbj = e.sb[EDGE ? min(j0 + jt, n - 1) : j0 + jt];  // past n: never stored
+        // pass column 64 wn + 32 yy + lane % 32, in buffer 4 wn + 2 yy + (lane & 16 ? 1 : 0): a select between
+        // two pointers, not a lane-indexed switch
+        const int b0 = 4 * wn + 2 * yy;
+        float *colp = ((lane & 16) ? stage_at(b0 + 1) : stage_at(b0)) + lc * 256;
 #pragma unroll
         for (int x = 0; x < 4; ++x)
 #pragma unroll
@@ -608,7 +620,9 @@ __device__ __forceinline__ float staged_general(const Epilogue &e, v16f (&acc)[4
     write_group(h, 1, cb, ca);
     write_group(h, 2, ca, cb);
     write_group(h, 3, cb, ca);
-  }
+  };
+  pass(std::integral_constant<int, 0>{});
+  pass(std::integral_constant<int, 1>{});
   return mx;
 }
 
