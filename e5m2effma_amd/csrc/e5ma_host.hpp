@@ -44,6 +44,8 @@ struct Tuning {
   int quant_grid = 8192;       // block cap of the per-tensor quantize's amax pass (its cast pass: cast_grid)
   int tail_half = 0;           // FP8 GEMM: 1 runs a last round of at most CUs / 2 tiles as 256 x 128 half tiles
                                // (the same bits either way; measured slower on the MI355X, so 0 there)
+  int gemv_rows = 2;           // GEMV n = 1 with a BF16 / FP8 x: rows per wave (1, 2 or 4; 8 / rows 16-byte chunks
+                               // per lane and batch).  Every choice sums each row in the same order: the same bits
 };
 
 struct DeviceInfo {

@@ -652,7 +652,7 @@ __global__ __launch_bounds__(kMThreads) void gemv_mfma_kernel(const uint8_t *A, 
 
 template <int AT, int BT, int NB>
 hipError_t gemv_n(const uint8_t *A, long long lda, const uint8_t *B, long long ldb, int m, int k, const Epilogue &e,
-                  hipStream_t s) {
+                  const Tuning &tu, hipStream_t s) {
   if constexpr (BT != E5MA_FP32 && NB >= E5MA_GEMV_MFMA_MIN_N) {
     gemv_mfma_kernel<AT, BT, NB, E5MA_GEMV_MFMA_U><<<(m + 15) / 16, kMThreads, 0, s>>>(A, lda, B, ldb, m, k, e);
     return hipGetLastError();
@@ -660,9 +660,21 @@ hipError_t gemv_n(const uint8_t *A, long long lda, const uint8_t *B, long long l
   if constexpr (BT != E5MA_FP32) {
     const long long xbytes = (long long)k * NB * elem_bytes(BT);
     if (xbytes <= kXLds) {
+      const size_t lds = (size_t)((xbytes + 1023) / 1024 * 1024);
+      if constexpr (NB == 1) {
+        // rows per wave from the tuned table (the tuner's candidates; every one sums a row in the same order)
+        if (tu.gemv_rows == 1) {
+          gemv_xlds_kernel<AT, BT, 1, 1, 8><<<(m + kXWaves - 1) / kXWaves, kXThreads, lds, s>>>(A, lda, B, ldb, m, k, e);
+          return hipGetLastError();
+        }
+        if (tu.gemv_rows == 4) {
+          gemv_xlds_kernel<AT, BT, 1, 4, 2><<<(m + 4 * kXWaves - 1) / (4 * kXWaves), kXThreads, lds, s>>>(A, lda, B, ldb,
+                                                                                                           m, k, e);
+          return hipGetLastError();
+        }
+      }
       constexpr int RX = NB <= 2 ? E5MA_GEMV_RX : kGemvRxWide<NB>, UX = NB <= 2 ? E5MA_GEMV_UX : kGemvUxWide;
       const int gx = (m + kXWaves * RX - 1) / (kXWaves * RX);
-      const size_t lds = (size_t)((xbytes + 1023) / 1024 * 1024);
       gemv_xlds_kernel<AT, BT, NB, RX, UX><<<gx, kXThreads, lds, s>>>(A, lda, B, ldb, m, k, e);
       return hipGetLastError();
     }
@@ -684,36 +696,36 @@ hipError_t gemv_n(const uint8_t *A, long long lda, const uint8_t *B, long long l
 
 template <int AT, int BT>
 hipError_t gemv_b(int n, const uint8_t *A, long long lda, const uint8_t *B, long long ldb, int m, int k,
-                  const Epilogue &e, hipStream_t s) {
+                  const Epilogue &e, const Tuning &tu, hipStream_t s) {
   switch (n) {
-    case 1: return gemv_n<AT, BT, 1>(A, lda, B, ldb, m, k, e, s);
-    case 2: return gemv_n<AT, BT, 2>(A, lda, B, ldb, m, k, e, s);
-    case 3: return gemv_n<AT, BT, 3>(A, lda, B, ldb, m, k, e, s);
-    case 4: return gemv_n<AT, BT, 4>(A, lda, B, ldb, m, k, e, s);
-    case 5: return gemv_n<AT, BT, 5>(A, lda, B, ldb, m, k, e, s);
-    case 6: return gemv_n<AT, BT, 6>(A, lda, B, ldb, m, k, e, s);
-    case 7: return gemv_n<AT, BT, 7>(A, lda, B, ldb, m, k, e, s);
-    default: return gemv_n<AT, BT, 8>(A, lda, B, ldb, m, k, e, s);
+    case 1: return gemv_n<AT, BT, 1>(A, lda, B, ldb, m, k, e, tu, s);
+    case 2: return gemv_n<AT, BT, 2>(A, lda, B, ldb, m, k, e, tu, s);
+    case 3: return gemv_n<AT, BT, 3>(A, lda, B, ldb, m, k, e, tu, s);
+    case 4: return gemv_n<AT, BT, 4>(A, lda, B, ldb, m, k, e, tu, s);
+    case 5: return gemv_n<AT, BT, 5>(A, lda, B, ldb, m, k, e, tu, s);
+    case 6: return gemv_n<AT, BT, 6>(A, lda, B, ldb, m, k, e, tu, s);
+    case 7: return gemv_n<AT, BT, 7>(A, lda, B, ldb, m, k, e, tu, s);
+    default: return gemv_n<AT, BT, 8>(A, lda, B, ldb, m, k, e, tu, s);
   }
 }
 
 template <int AT>
 hipError_t gemv_a(int bt, int n, const uint8_t *A, long long lda, const uint8_t *B, long long ldb, int m, int k,
-                  const Epilogue &e, hipStream_t s) {
+                  const Epilogue &e, const Tuning &tu, hipStream_t s) {
   switch (bt) {
-    case E5MA_E5M2: return gemv_b<AT, E5MA_E5M2>(n, A, lda, B, ldb, m, k, e, s);
-    case E5MA_E4M3: return gemv_b<AT, E5MA_E4M3>(n, A, lda, B, ldb, m, k, e, s);
-    case E5MA_BF16: return gemv_b<AT, E5MA_BF16>(n, A, lda, B, ldb, m, k, e, s);
-    default: return gemv_b<AT, E5MA_FP32>(n, A, lda, B, ldb, m, k, e, s);
+    case E5MA_E5M2: return gemv_b<AT, E5MA_E5M2>(n, A, lda, B, ldb, m, k, e, tu, s);
+    case E5MA_E4M3: return gemv_b<AT, E5MA_E4M3>(n, A, lda, B, ldb, m, k, e, tu, s);
+    case E5MA_BF16: return gemv_b<AT, E5MA_BF16>(n, A, lda, B, ldb, m, k, e, tu, s);
+    default: return gemv_b<AT, E5MA_FP32>(n, A, lda, B, ldb, m, k, e, tu, s);
   }
 }
 
 }  // namespace
 
 hipError_t launch_gemv(int at, int bt, const uint8_t *A, long long lda, const uint8_t *B, long long ldb, int m, int n,
-                       int k, const Epilogue &e, const DeviceInfo &, hipStream_t s) {
-  if (at == E5MA_E5M2) return gemv_a<E5MA_E5M2>(bt, n, A, lda, B, ldb, m, k, e, s);
-  return gemv_a<E5MA_E4M3>(bt, n, A, lda, B, ldb, m, k, e, s);
+                       int k, const Epilogue &e, const DeviceInfo &di, hipStream_t s) {
+  if (at == E5MA_E5M2) return gemv_a<E5MA_E5M2>(bt, n, A, lda, B, ldb, m, k, e, di.tune, s);
+  return gemv_a<E5MA_E4M3>(bt, n, A, lda, B, ldb, m, k, e, di.tune, s);
 }
 
 }  // namespace e5ma

@@ -8,7 +8,8 @@
 // candidate's on varied inputs; one that differs is reported and never picked.
 //
 //   e5ma_tune [header] [--dry-run]       tune, print the entry, and (unless --dry-run) rewrite header
-//   e5ma_tune --emit header arch cus splitk_div cast_grid adam_grid_bf16 adam_grid_fp32 quant_grid tail_half [name]
+//   e5ma_tune --emit header arch cus splitk_div cast_grid adam_grid_bf16 adam_grid_fp32 quant_grid tail_half gemv_rows
+//                [name]
 //                                        rewrite header with that entry, no device use (tests)
 //   e5ma_tune --ceiling                  AdamW over 2^28 parameters beside a kernel with the same memory
 //                                        accesses and no arithmetic (the access pattern's own ceiling)
@@ -23,6 +24,9 @@
 //   tail_half       0 / 1: TE wgrad (N, T) 14336 x 4096 x 8192 into FP32 with beta = 1 (896 tiles: a half-full
 //                   last round) and a half-filled grid, E5M2 x E4M3 -> BF16 TN 4096 x 2048 x 8192 (summed);
 //                   the candidates' outputs are compared bit for bit (half tiles must not change results)
+//   gemv_rows       1 / 2 / 4 rows per wave of the n = 1 GEMV with a BF16 x: 8192 x 8192 E5M2 weights with row
+//                   scales, 6 buffers rotated; outputs compared bit for bit (every choice sums a row in the same
+//                   order).  The n >= 2 GEMV shapes change the summation order, so they stay compile-time choices
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdio.h>
@@ -358,8 +362,60 @@ static Tuning tune_device(const DeviceInfo &di) {
     }
     for (void *b : {(void *)A, (void *)B, D}) check(hipFree(b), "hipFree");
   }
-  printf("outputs of %d cast / quantize / half-tile candidates compared with their first candidate's: %d differ\n", checked,
-         differing);
+  // ---- GEMV n = 1 rows per wave (results must not change) ----
+  {
+    const int M = 8192, K = 8192, nbuf = 6;  // 6 x 64 MiB of weights, rotated past the Infinity Cache
+    std::vector<uint8_t *> W;
+    for (int b = 0; b < nbuf; ++b) {
+      W.push_back((uint8_t *)dalloc((size_t)M * K, 0));
+      fill_codes(W.back(), (size_t)M * K, 20 + b, E5MA_E5M2);
+    }
+    std::vector<uint16_t> xh(K);
+    for (int i = 0; i < K; ++i) xh[i] = (uint16_t)(0x3C00 + (i * 37 % 512) + (i % 3 == 0 ? 0x8000 : 0));  // BF16 x
+    void *x = dalloc((size_t)K * 2, 0), *y = dalloc((size_t)M * 2, 0);
+    check(hipMemcpy(x, xh.data(), xh.size() * 2, hipMemcpyHostToDevice), "hipMemcpy");
+    std::vector<float> sah(M);
+    for (int i = 0; i < M; ++i) sah[i] = ldexpf(1.f, -6 - i % 5);
+    float *sa = (float *)dalloc((size_t)M * 4, 0);
+    check(hipMemcpy(sa, sah.data(), sah.size() * 4, hipMemcpyHostToDevice), "hipMemcpy");
+    const std::vector<int> cands = {2, 1, 4};  // the default first: the others are compared with it
+    std::vector<float> ms;
+    std::vector<bool> ok(cands.size(), true);
+    std::vector<uint8_t> first;
+    for (size_t c = 0; c < cands.size(); ++c) {
+      DeviceInfo x1 = di;
+      x1.tune = def;
+      x1.tune.gemv_rows = cands[c];
+      dev::Epilogue e{};
+      e.alpha = 1.f;
+      e.sa = sa;
+      e.sa_vec = 1;
+      e.d = y;
+      e.ldd = M;
+      e.d_dtype = E5MA_BF16;
+      e.c_dtype = E5MA_FP32;
+      e.bias_dtype = E5MA_FP32;
+      auto run = [&](int i) {
+        return launch_gemv(E5MA_E5M2, E5MA_BF16, W[i % nbuf], K, (const uint8_t *)x, K, M, 1, K, e, x1, nullptr);
+      };
+      check(run(0), "launch");
+      check(hipDeviceSynchronize(), "hipDeviceSynchronize");
+      std::vector<uint8_t> got = fetch(y, (size_t)M * 2);
+      if (c == 0) first = got;
+      else if (got != first) ok[c] = false;
+      ms.push_back(best_ms(run, 30));
+    }
+    printf("GEMV n = 1, 8192 x 8192 E5M2 (row scales) x BF16 -> BF16, weights rotated over 6 buffers\n");
+    t.gemv_rows = pick("gemv_rows", cands, ms, def.gemv_rows, ok);
+    for (size_t c = 1; c < cands.size(); ++c) {
+      ++checked;
+      if (!ok[c]) ++differing;
+    }
+    for (uint8_t *b : W) check(hipFree(b), "hipFree");
+    for (void *b : {x, y, (void *)sa}) check(hipFree(b), "hipFree");
+  }
+  printf("outputs of %d cast / quantize / half-tile / GEMV candidates compared with their first candidate's: %d differ\n",
+         checked, differing);
   return t;
 }
 
@@ -379,8 +435,9 @@ static int emit(const char *path, const char *arch, int cus, const Tuning &t, co
     }
   }
   char buf[512];
-  snprintf(buf, sizeof buf, "  {\"%s\", %d, {%d, %d, %d, %d, %d, %d}}, /* entry arch=%s cus=%d tuned on %s */ \\", arch,
-           cus, t.splitk_div, t.cast_grid, t.adam_grid_bf16, t.adam_grid_fp32, t.quant_grid, t.tail_half, arch, cus, name);
+  snprintf(buf, sizeof buf, "  {\"%s\", %d, {%d, %d, %d, %d, %d, %d, %d}}, /* entry arch=%s cus=%d tuned on %s */ \\",
+           arch, cus, t.splitk_div, t.cast_grid, t.adam_grid_bf16, t.adam_grid_fp32, t.quant_grid, t.tail_half, t.gemv_rows,
+           arch, cus, name);
   keep.push_back(buf);
   std::ofstream out(path);
   if (!out) {
@@ -389,8 +446,8 @@ static int emit(const char *path, const char *arch, int cus, const Tuning &t, co
   }
   out << "// e5ma_tuned.h -- written by the tuner (e5m2effma_amd/tune/tune.cpp; make -C e5m2effma_amd/csrc tune-run):\n"
          "// per-device launch choices of struct Tuning (e5ma_host.hpp), one entry per (architecture, CU count):\n"
-         "// {arch, cus, {splitk_div, cast_grid, adam_grid_bf16, adam_grid_fp32, quant_grid, tail_half}}.  Re-running the\n"
-         "// tuner on a device adds or replaces that device's entry and keeps the others.\n"
+         "// {arch, cus, {splitk_div, cast_grid, adam_grid_bf16, adam_grid_fp32, quant_grid, tail_half, gemv_rows}}.\n"
+         "// Re-running the tuner on a device adds or replaces that device's entry and keeps the others.\n"
          "#pragma once\n#define E5MA_TUNED_ENTRIES \\\n";
   for (const std::string &l : keep) out << l << "\n";
   out << "\n";
@@ -399,7 +456,7 @@ static int emit(const char *path, const char *arch, int cus, const Tuning &t, co
 }
 
 int main(int argc, char **argv) {
-  if (argc >= 11 && strcmp(argv[1], "--emit") == 0) {
+  if (argc >= 12 && strcmp(argv[1], "--emit") == 0) {
     Tuning t;
     t.splitk_div = atoi(argv[5]);
     t.cast_grid = atoi(argv[6]);
@@ -407,7 +464,8 @@ int main(int argc, char **argv) {
     t.adam_grid_fp32 = atoi(argv[8]);
     t.quant_grid = atoi(argv[9]);
     t.tail_half = atoi(argv[10]);
-    return emit(argv[2], argv[3], atoi(argv[4]), t, argc > 11 ? argv[11] : "unnamed device");
+    t.gemv_rows = atoi(argv[11]);
+    return emit(argv[2], argv[3], atoi(argv[4]), t, argc > 12 ? argv[12] : "unnamed device");
   }
   const char *path = "e5m2effma_amd/csrc/e5ma_tuned.h";
   bool dry = false, ceil_only = false;
@@ -439,7 +497,7 @@ int main(int argc, char **argv) {
   }
   printf("tuning on %s (%s, %d CUs)\n", name, arch, di.cus);
   const Tuning t = tune_device(di);
-  printf("entry: {\"%s\", %d, {%d, %d, %d, %d, %d, %d}}\n", arch, di.cus, t.splitk_div, t.cast_grid, t.adam_grid_bf16,
-         t.adam_grid_fp32, t.quant_grid, t.tail_half);
+  printf("entry: {\"%s\", %d, {%d, %d, %d, %d, %d, %d, %d}}\n", arch, di.cus, t.splitk_div, t.cast_grid,
+         t.adam_grid_bf16, t.adam_grid_fp32, t.quant_grid, t.tail_half, t.gemv_rows);
   return dry ? 0 : emit(path, arch, di.cus, t, name);
 }

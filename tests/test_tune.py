@@ -12,18 +12,18 @@ import pytest
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 CSRC = os.path.join(ROOT, "e5m2effma_amd", "csrc")
 TUNER = os.path.join(ROOT, "e5m2effma_amd", "tune", "e5ma_tune")
-ENTRY = re.compile(r'\{"(\w+)", (\d+), \{(-?\d+), (\d+), (\d+), (\d+), (\d+), (\d+)\}\}, /\* entry arch=(\w+) cus=(\d+) ')
+ENTRY = re.compile(r'\{"(\w+)", (\d+), \{(-?\d+), (\d+), (\d+), (\d+), (\d+), (\d+), (\d+)\}\}, /\* entry arch=(\w+) cus=(\d+) ')
 
 
 def entries(path):
     with open(path) as f:
-        return [m.groups()[:8] for m in map(ENTRY.search, f) if m]
+        return [m.groups()[:9] for m in map(ENTRY.search, f) if m]
 
 
 def compiles(path, tmp_path, count):
     src = tmp_path / "t.cpp"
     src.write_text('struct Tuning { int splitk_div = 4, cast_grid = 8192, adam_grid_bf16 = 65536, adam_grid_fp32 = 8192, '
-                   'quant_grid = 8192, tail_half = 1; };\n'
+                   'quant_grid = 8192, tail_half = 1, gemv_rows = 2; };\n'
                    'struct TunedEntry { const char *arch; int cus; Tuning t; };\n'
                    f'#include "{path}"\n'
                    'static const TunedEntry kTuned[] = {E5MA_TUNED_ENTRIES{nullptr, 0, {}}};\n'
@@ -47,12 +47,12 @@ def test_emit_adds_replaces_and_keeps(tmp_path):
     shutil.copy(os.path.join(CSRC, "e5ma_tuned.h"), h)
     before = entries(h)
     run = lambda *a: subprocess.run([TUNER, "--emit", str(h), *map(str, a)], check=True, capture_output=True, env={})
-    run("gfx942", 304, 2, 4096, 32768, 8192, 4096, 0, "another device")
+    run("gfx942", 304, 2, 4096, 32768, 8192, 4096, 0, 1, "another device")
     es = entries(h)
-    assert es[:len(before)] == before and es[-1] == ("gfx942", "304", "2", "4096", "32768", "8192", "4096", "0")
-    run("gfx950", 256, 8, 16384, 131072, 4096, 2048, 1, "MI355X")
+    assert es[:len(before)] == before and es[-1] == ("gfx942", "304", "2", "4096", "32768", "8192", "4096", "0", "1")
+    run("gfx950", 256, 8, 16384, 131072, 4096, 2048, 1, 4, "MI355X")
     es = entries(h)
-    assert ("gfx942", "304", "2", "4096", "32768", "8192", "4096", "0") in es
-    assert [e for e in es if e[:2] == ("gfx950", "256")] == [("gfx950", "256", "8", "16384", "131072", "4096", "2048", "1")]
+    assert ("gfx942", "304", "2", "4096", "32768", "8192", "4096", "0", "1") in es
+    assert [e for e in es if e[:2] == ("gfx950", "256")] == [("gfx950", "256", "8", "16384", "131072", "4096", "2048", "1", "4")]
     ok, err = compiles(str(h), tmp_path, len(es))
     assert ok, err
