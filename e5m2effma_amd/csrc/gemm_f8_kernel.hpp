@@ -306,17 +306,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_f8_kernel(TileArgs t0, Epilo
   float sa1, sb1;  // per-tensor scales: the same for every tile and split
   epilogue_scales(e0, sa1, sb1);
   float mx = 0.f;
-  {
-    // A block with no tile in the launch's last round (a partly filled last round) starts about half a tile
-    // late: the write-outs of the two groups of blocks then come at different times instead of all at once
-    // (TE wgrad 14336 x 4096 x 8192, 896 tiles: 417.7 -> 409.4 us), and the late blocks still finish first.
-    const int mine = (t0.count - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x;
-    const int most = (t0.count + (int)gridDim.x - 1) / (int)gridDim.x;
-    if (mine < most) {
-      const unsigned long long s0 = __builtin_amdgcn_s_memtime(), wait = 512ull * (t0.k / kUnitK);
-      while (__builtin_amdgcn_s_memtime() - s0 < wait) __builtin_amdgcn_s_sleep(32);
-    }
-  }
+  late_start(t0, 512ull * (t0.k / kUnitK));  // about half a tile: 16 MFMAs of 64 cycles per unit, half of them
   for (int blk = blockIdx.x; blk < t0.count; blk += gridDim.x) {
     // lane and thread ids made opaque per tile, so that nothing derived from them is hoisted out of the tile
     // loop and kept live across the K loop (that spilled 184 bytes)

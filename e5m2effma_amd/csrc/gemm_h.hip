@@ -20,7 +20,7 @@ bool gemm_h_applies(int at, int bt, bool akc, bool bkc, int m, int n, int k) {
 hipError_t launch_gemm_h(int at, int bt, bool akc, bool bkc, const uint8_t *A, long long lda, const uint8_t *B,
                          long long ldb, int m, int n, int k, int splits, int cus, int tail_half, const dev::Epilogue &e,
                          hipStream_t s) {
-  // (cus, tail_half: the BF16-core kernel runs one tile per block, whole)
+  // (tail_half: the BF16-core kernel runs whole tiles only; cus: its persistent grid)
   if (bt == E5MA_BF16)
     return (akc ? launch_gemm_h_tn_bf16 : launch_gemm_h_nn_bf16)(at, bt, A, lda, B, ldb, m, n, k, splits, cus, tail_half, e, s);
   if (akc) return (bkc ? launch_gemm_h_tn : launch_gemm_h_tt)(at, bt, A, lda, B, ldb, m, n, k, splits, cus, tail_half, e, s);

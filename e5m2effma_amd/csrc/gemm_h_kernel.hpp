@@ -183,65 +183,76 @@ __device__ __forceinline__ void h_stage(const TileArgs &t, int s, int i0, int j0
 }
 
 template <int AT, int BT, bool AKC, bool BKC, int EPI>
-__global__ __launch_bounds__(kThreads, 1) void gemm_h_kernel(TileArgs t, Epilogue e, int simple, int vec) {
+__global__ __launch_bounds__(kThreads, 1) void gemm_h_kernel(TileArgs t0, Epilogue e0, int simple, int vec) {
   using C = Cfg<AT, BT, AKC, BKC>;
   __shared__ float red[kThreads / 64];
-  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int tid0 = threadIdx.x, lane0 = tid0 & 63, wave = __builtin_amdgcn_readfirstlane(tid0 >> 6);
   const int wm = wave >> 1, wn = wave & 1;
-  int tm, tn, sp;
-  tile_of(blockIdx.x, t, tm, tn, sp);
-  apply_split(t, e, sp);
-  const int i0 = tm * kBM, j0 = tn * kBN;
-  const int nk = t.k / C::KS;
+  float sa1, sb1;  // per-tensor scales: the same for every tile and split
+  epilogue_scales(e0, sa1, sb1);
+  float mx = 0.f;
+  // a stage is KS k of 16 MFMAs of 32 cycles per 16 k per wave: about half a tile is 256 cycles per k-step
+  late_start(t0, 256ull * (t0.k / 16));
+  for (int blk = blockIdx.x; blk < t0.count; blk += gridDim.x) {
+    // lane and thread ids made opaque per tile, so that nothing derived from them is hoisted out of the tile loop
+    int lane = lane0, tid = tid0;
+    asm volatile("" : "+v"(lane), "+v"(tid));
+    TileArgs t = t0;
+    Epilogue e = e0;
+    int tm, tn, sp;
+    tile_of(blk, t, tm, tn, sp);
+    apply_split(t, e, sp);
+    const int i0 = tm * kBM, j0 = tn * kBN;
+    const int nk = t.k / C::KS;
 
-  float sa1, sb1;
-  epilogue_scales(e, sa1, sb1);
+    v16f acc[4][4];
+#pragma unroll
+    for (int x = 0; x < 4; ++x)
+#pragma unroll
+      for (int y = 0; y < 4; ++y)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[x][y][r] = 0.f;
 
-  v16f acc[4][4];
+    // prologue: stages 0..2 in flight; stage 3 is issued once every wave is past the first barrier
 #pragma unroll
-  for (int x = 0; x < 4; ++x)
+    for (int x = 0; x < 4; ++x) issue_part<C, 0, AKC, BKC>(t, 0, i0, j0, wave, lane, x);
 #pragma unroll
-    for (int y = 0; y < 4; ++y)
+    for (int x = 0; x < 4; ++x) issue_part<C, 1, AKC, BKC>(t, 1, i0, j0, wave, lane, x);
 #pragma unroll
-      for (int r = 0; r < 16; ++r) acc[x][y][r] = 0.f;
+    for (int x = 0; x < 4; ++x) issue_part<C, 2, AKC, BKC>(t, 2, i0, j0, wave, lane, x);
+    wait_barrier<2 * C::kLoads>();  // stage 0 landed; stages 1 and 2 may be in flight
+#pragma unroll
+    for (int x = 0; x < 4; ++x) issue_part<C, 3, AKC, BKC>(t, 3, i0, j0, wave, lane, x);
+    typename C::FA a[4];
+    typename C::FB b[4];
+#pragma unroll
+    for (int x = 0; x < 4; ++x) {
+      read_frag(a[x], lds_a<0>(), 128 * wm + 32 * x, lane);
+      read_frag(b[x], lds_b<0>(), 128 * wn + 32 * x, lane);
+    }
+    constexpr int kW2 = 2 * C::kLoads, kW1 = C::kLoads;
+    int s = 0;
+    for (; s < nk - 4; s += 4) {
+      h_stage<C, kW2, true, true, 0, AT, BT, AKC, BKC>(t, s, i0, j0, wave, lane, wm, wn, a, b, acc);
+      h_stage<C, kW2, true, true, 1, AT, BT, AKC, BKC>(t, s + 1, i0, j0, wave, lane, wm, wn, a, b, acc);
+      h_stage<C, kW2, true, true, 2, AT, BT, AKC, BKC>(t, s + 2, i0, j0, wave, lane, wm, wn, a, b, acc);
+      h_stage<C, kW2, true, true, 3, AT, BT, AKC, BKC>(t, s + 3, i0, j0, wave, lane, wm, wn, a, b, acc);
+    }
+    h_stage<C, kW2, true, false, 0, AT, BT, AKC, BKC>(t, s, i0, j0, wave, lane, wm, wn, a, b, acc);
+    h_stage<C, kW1, true, false, 1, AT, BT, AKC, BKC>(t, s + 1, i0, j0, wave, lane, wm, wn, a, b, acc);
+    h_stage<C, 0, true, false, 2, AT, BT, AKC, BKC>(t, s + 2, i0, j0, wave, lane, wm, wn, a, b, acc);
+    h_stage<C, 0, false, false, 3, AT, BT, AKC, BKC>(t, s + 3, i0, j0, wave, lane, wm, wn, a, b, acc);
 
-  // prologue: stages 0..2 in flight; stage 3 is issued once every wave is past the first barrier
-#pragma unroll
-  for (int x = 0; x < 4; ++x) issue_part<C, 0, AKC, BKC>(t, 0, i0, j0, wave, lane, x);
-#pragma unroll
-  for (int x = 0; x < 4; ++x) issue_part<C, 1, AKC, BKC>(t, 1, i0, j0, wave, lane, x);
-#pragma unroll
-  for (int x = 0; x < 4; ++x) issue_part<C, 2, AKC, BKC>(t, 2, i0, j0, wave, lane, x);
-  wait_barrier<2 * C::kLoads>();  // stage 0 landed; stages 1 and 2 may be in flight
-#pragma unroll
-  for (int x = 0; x < 4; ++x) issue_part<C, 3, AKC, BKC>(t, 3, i0, j0, wave, lane, x);
-  typename C::FA a[4];
-  typename C::FB b[4];
-#pragma unroll
-  for (int x = 0; x < 4; ++x) {
-    read_frag(a[x], lds_a<0>(), 128 * wm + 32 * x, lane);
-    read_frag(b[x], lds_b<0>(), 128 * wn + 32 * x, lane);
+    mx = fmaxf(mx, tile_epilogue<EPI>(t, e, acc, i0, j0, wm, wn, lane, tid, simple, vec, sa1, sb1));
+    __syncthreads();  // the write-out's ring reads are done before the next tile's loads refill the ring
   }
-  constexpr int kW2 = 2 * C::kLoads, kW1 = C::kLoads;
-  int s = 0;
-  for (; s < nk - 4; s += 4) {
-    h_stage<C, kW2, true, true, 0, AT, BT, AKC, BKC>(t, s, i0, j0, wave, lane, wm, wn, a, b, acc);
-    h_stage<C, kW2, true, true, 1, AT, BT, AKC, BKC>(t, s + 1, i0, j0, wave, lane, wm, wn, a, b, acc);
-    h_stage<C, kW2, true, true, 2, AT, BT, AKC, BKC>(t, s + 2, i0, j0, wave, lane, wm, wn, a, b, acc);
-    h_stage<C, kW2, true, true, 3, AT, BT, AKC, BKC>(t, s + 3, i0, j0, wave, lane, wm, wn, a, b, acc);
-  }
-  h_stage<C, kW2, true, false, 0, AT, BT, AKC, BKC>(t, s, i0, j0, wave, lane, wm, wn, a, b, acc);
-  h_stage<C, kW1, true, false, 1, AT, BT, AKC, BKC>(t, s + 1, i0, j0, wave, lane, wm, wn, a, b, acc);
-  h_stage<C, 0, true, false, 2, AT, BT, AKC, BKC>(t, s + 2, i0, j0, wave, lane, wm, wn, a, b, acc);
-  h_stage<C, 0, false, false, 3, AT, BT, AKC, BKC>(t, s + 3, i0, j0, wave, lane, wm, wn, a, b, acc);
-
-  const float mx = tile_epilogue<EPI>(t, e, acc, i0, j0, wm, wn, lane, tid, simple, vec, sa1, sb1);
-  if (e.amax) amax_commit_block(e.amax, mx, red);
+  if (e0.amax) amax_commit_block(e0.amax, mx, red);
 }
 
 template <int AT, int BT, bool AKC, bool BKC>
-hipError_t run_d(const TileArgs &t, const Epilogue &e, hipStream_t s) {
-  const int grid = t.tiles_m * t.tiles_n * t.splits;
+hipError_t run_d(const TileArgs &t, const Epilogue &e, int cus, hipStream_t s) {
+  // persistent: at most one block per CU (cus > 0), each looping over its tiles in the XCD-aware order
+  const int whole = t.tiles_m * t.tiles_n * t.splits, grid = cus > 0 && whole > cus ? cus : whole;
   const int vec = ((uintptr_t)e.d % (4 * elem_bytes(e.d_dtype))) == 0 && e.ldd % 4 == 0 &&
                   (!e.sa_vec || (uintptr_t)e.sa % 16 == 0);
   const int simple = e.bias == nullptr && e.beta == 0.f && vec;
@@ -256,25 +267,28 @@ hipError_t run_d(const TileArgs &t, const Epilogue &e, hipStream_t s) {
 // the FP8 A x FP8 B pairings for one layout pair (lda / ldb in elements; splits as in the FP8 kernel)
 template <bool AKC, bool BKC>
 hipError_t launch_layout(int at, int bt, const uint8_t *A, long long lda, const uint8_t *B, long long ldb, int m, int n,
-                         int k, int splits, const Epilogue &e, hipStream_t s) {
+                         int k, int splits, int cus, const Epilogue &e, hipStream_t s) {
   const int ks = k / splits;
   const int tm = (m + kBM - 1) / kBM, tn = (n + kBN - 1) / kBN;
   const TileArgs t{A, B, lda, ldb, m, n, ks, tm, tn, splits, AKC ? ks : ks * lda, BKC ? ks : ks * ldb, e.ldd * n * 4,
                    0, tm * tn * splits};
   if (at == E5MA_E5M2)
-    return bt == E5MA_E5M2 ? run_d<E5MA_E5M2, E5MA_E5M2, AKC, BKC>(t, e, s) : run_d<E5MA_E5M2, E5MA_E4M3, AKC, BKC>(t, e, s);
-  return bt == E5MA_E5M2 ? run_d<E5MA_E4M3, E5MA_E5M2, AKC, BKC>(t, e, s) : run_d<E5MA_E4M3, E5MA_E4M3, AKC, BKC>(t, e, s);
+    return bt == E5MA_E5M2 ? run_d<E5MA_E5M2, E5MA_E5M2, AKC, BKC>(t, e, cus, s)
+                           : run_d<E5MA_E5M2, E5MA_E4M3, AKC, BKC>(t, e, cus, s);
+  return bt == E5MA_E5M2 ? run_d<E5MA_E4M3, E5MA_E5M2, AKC, BKC>(t, e, cus, s)
+                         : run_d<E5MA_E4M3, E5MA_E4M3, AKC, BKC>(t, e, cus, s);
 }
 
 // FP8 A x K-contiguous BF16 B (ldb in elements)
 template <bool AKC>
-hipError_t launch_layout_bf16(int at, int, const uint8_t *A, long long lda, const uint8_t *B, long long ldb, int m, int n,
-                              int k, int splits, const Epilogue &e, hipStream_t s) {
+hipError_t launch_layout_bf16(int at, int, const uint8_t *A, long long lda, const uint8_t *B, long long ldb, int m,
+                              int n, int k, int splits, int cus, const Epilogue &e, hipStream_t s) {
   const int ks = k / splits;
   const int tm = (m + kBM - 1) / kBM, tn = (n + kBN - 1) / kBN;
   const TileArgs t{A, B, lda, 2 * ldb, m, n, ks, tm, tn, splits, AKC ? ks : ks * lda, 2LL * ks, e.ldd * n * 4,
                    0, tm * tn * splits};
-  return at == E5MA_E5M2 ? run_d<E5MA_E5M2, E5MA_BF16, AKC, true>(t, e, s) : run_d<E5MA_E4M3, E5MA_BF16, AKC, true>(t, e, s);
+  return at == E5MA_E5M2 ? run_d<E5MA_E5M2, E5MA_BF16, AKC, true>(t, e, cus, s)
+                         : run_d<E5MA_E4M3, E5MA_BF16, AKC, true>(t, e, cus, s);
 }
 
 }  // namespace hk

@@ -2,5 +2,5 @@
 #include "gemm_h_kernel.hpp"
 
 namespace e5ma {
-E5MA_F8_LAYOUT_DECL(launch_gemm_h_tt) { return hk::launch_layout<true, false>(at, bt, A, lda, B, ldb, m, n, k, splits, e, s); }
+E5MA_F8_LAYOUT_DECL(launch_gemm_h_tt) { return hk::launch_layout<true, false>(at, bt, A, lda, B, ldb, m, n, k, splits, cus, e, s); }
 }  // namespace e5ma

@@ -734,6 +734,19 @@ __device__ __forceinline__ float staged_full(const Epilogue &e, v16f (&acc)[4][4
   return staged_general<kAnyD, kAnyC, EDGE>(e, acc, i0, j0, m, n, wm, wn, lane, tid, sa1, sb1);
 }
 
+// Persistent launches (block b takes tiles b, b + gridDim.x, ...): a block with no tile in the launch's last
+// round (a partly filled last round) starts about half a tile late, waiting wait_cycles on the shader clock.
+// The write-outs of the two groups of blocks then come at different times instead of all at once (TE wgrad
+// 14336 x 4096 x 8192, 896 tiles: 417.7 -> 409.4 us), and the late blocks still finish first.
+__device__ __forceinline__ void late_start(const TileArgs &t, unsigned long long wait_cycles) {
+  const int mine = (t.count - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x;
+  const int most = (t.count + (int)gridDim.x - 1) / (int)gridDim.x;
+  if (mine < most) {
+    const unsigned long long s0 = __builtin_amdgcn_s_memtime();
+    while (__builtin_amdgcn_s_memtime() - s0 < wait_cycles) __builtin_amdgcn_s_sleep(32);
+  }
+}
+
 // The epilogue of a block tile (acc: this wave's accumulators; i0, j0: the tile's origin; sa1 = alpha * sa
 // and sb1 = sb, the per-tensor scales read before the K loop) for D of any dtype (e.d_dtype), in class
 // EPI.  Returns the thread's max |value| for amax.
