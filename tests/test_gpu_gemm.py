@@ -378,6 +378,20 @@ def test_fast_unsplit_h_sampled(dev):
     assert bad == 0, first
 
 
+@pytest.mark.parametrize("k,ta,tb,ddt", [(8192, 1, 0, B16), (8192, 0, 1, F32), (1024, 1, 0, B16), (1024, 0, 0, F32)])
+def test_persistent_partial_last_round(dev, k, ta, tb, ddt):
+    """4608 x 4352 = 18 x 17 = 306 tiles on a persistent grid of one block per CU: 50 blocks take two tiles
+    and the other blocks, with no tile in the last round, start late.  FP8 matrix cores (k = 8192) and BF16
+    ones (k = 1024); the BF16 write-out and the full one (FP32 D, bias, beta * BF16 C); sampled against the
+    oracle's bound, the padding rows of D untouched."""
+    rng = np.random.default_rng(9900 + k + 2 * ta + tb + ddt)
+    kw = dict(biasdt=F32, beta=0.5, cdt=B16) if ddt == F32 else {}
+    case = gu.GemmCase(rng, ta, tb, 4608, 4352, k, E5, E4, ddt=ddt, dist="normal", sigma=2.0, sa=0.5, sb=0.25,
+                       pad=0, ldd=4608 + 8, **kw)
+    bad, first = case.run_and_check(dev, samples=4096, rng=rng)
+    assert bad == 0, first
+
+
 @pytest.mark.parametrize("m,n,k,adt,bdt", [(8192, 32, 8192, E5, E4), (256, 256, 16384, E4, E5),
                                             (1024, 8192, 8192, E5, E5), (64, 48, 512, E5, E4),
                                             (130, 20, 768, E4, B16)])
