@@ -146,12 +146,12 @@ def counter_means(counters_csv):
     return kern
 
 
-# The kernels (short name, grid) one launch of each workload runs, at bench.py's shapes (the FP8 GEMM kernel
-# is persistent: at most one block per CU, 256 on the MI355X)
+# The kernels (short name, grid) one launch of each workload runs, at bench.py's shapes (the GEMM kernels are
+# persistent: at most one block per CU, 256 on the MI355X)
 WORKLOAD_KERNELS = {
     "gemm_8192_e5m2xe4m3": [("f8k::gemm_f8_kernel<4, 0, true, true, 0>", 256)],
     "gemm_8192_e5m2xe5m2": [("f8k::gemm_f8_kernel<4, 4, true, true, 0>", 256)],
-    "gemm_8192_e5m2xbf16": [("hk::gemm_h_kernel<4, 1, true, true, 0>", 1024)],
+    "gemm_8192_e5m2xbf16": [("hk::gemm_h_kernel<4, 1, true, true, 0>", 256)],
     "gemm_8192_nn": [("f8k::gemm_f8_kernel<4, 0, false, true, 0>", 256)],
     "gemm_8192_nt": [("f8k::gemm_f8_kernel<4, 0, false, false, 0>", 256)],
     "gemm_8192_tt": [("f8k::gemm_f8_kernel<4, 0, true, false, 0>", 256)],
