@@ -35,13 +35,13 @@ __global__ __launch_bounds__(kThreads) void cast_kernel(const void *__restrict__
       Pack<TI, kVec, E5MA_CAST_NT_IN> in;
       in.load(src, c * kVec);
       Pack<TO, kVec, E5MA_CAST_NT_OUT> out;
-      out.clear();
+      float v[kVec];
 #pragma unroll
       for (int e = 0; e < kVec; ++e) {
-        const float v = in.get(e, sinv);
-        if constexpr (AMAX) mx = amax_fold(mx, v);
-        out.put(e, v, qs);
+        v[e] = in.get(e, sinv);
+        if constexpr (AMAX) mx = amax_fold(mx, v[e]);
       }
+      out.set(v, qs);
       out.store(dst, c * kVec);
     }
     tail = nvec * kVec;

@@ -57,26 +57,35 @@ __device__ __forceinline__ uint32_t f32_to_f16(float x) {
   asm volatile("" : "+v"(x));
   return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x);
 }
-// FP32 -> FP8 with MB mantissa bits and exponent bias BIAS: round to nearest even, |x| >= the largest
-// finite value (Inf included) saturates to it, every NaN -> 0x7F (sign dropped).  The semantics of
-// cvt.rn.satfinite used by the reference (src/e5m2effma.cuh:90-124).
-template <int MB, int BIAS, uint32_t MAXBITS, uint32_t MAXCODE>
-__device__ __forceinline__ uint32_t f32_to_fp8(float x) {
-  const uint32_t u = f2u(x), s = (u >> 24) & 0x80u, a = u & 0x7FFFFFFFu;
-  if (a > 0x7F800000u) return 0x7Fu;
-  if (a >= MAXBITS) return s | MAXCODE;
-  constexpr uint32_t kMinNormal = (uint32_t)(128 - BIAS) << 23;
-  if (a < kMinNormal) {
-    // subnormal grid 2^(1 - BIAS - MB): scale by 2^(BIAS - 1 + MB) (exact), round half to even
-    const float q = __builtin_rintf(u2f(a) * (float)(1u << (BIAS - 1 + MB)));
-    return s | (uint32_t)q;
-  }
-  constexpr int kDrop = 23 - MB;
-  const uint32_t r = a + ((1u << (kDrop - 1)) - 1u) + ((a >> kDrop) & 1u);
-  return s | ((r >> kDrop) - ((uint32_t)(127 - BIAS) << MB));
+// FP32 -> FP8 codes (E5M2: v_cvt_pk_bf8_f32, E4M3: v_cvt_pk_fp8_f32): round to nearest even, |x| >= the
+// largest finite value (Inf included) saturates to it, every NaN -> 0x7F (sign dropped) -- the semantics of
+// cvt.rn.satfinite used by the reference (src/e5m2effma.cuh:90-124).  The instructions do not saturate, so
+// the input is first clamped to [-max, max] (v_med3_f32), and NaN is selected apart.  Equal, for every one of
+// the 2^32 FP32 inputs, to the integer formulation rounding the significand at bit 23 - mantissa bits (with a
+// subnormal grid of 2^(1 - bias - mantissa bits)), which this library used before: compared exhaustively on
+// gfx950, both encoders and both words of the pair instruction.
+template <int T> constexpr float kFp8Max = T == E5MA_E5M2 ? 57344.f : 448.f;
+// codes of a and b into word HI of old (bytes 2 HI, 2 HI + 1), the other word kept
+template <int T, bool HI> __device__ __forceinline__ uint32_t fp8_pair_into(float a, float b, uint32_t old) {
+  const float ca = __builtin_amdgcn_fmed3f(a, -kFp8Max<T>, kFp8Max<T>);
+  const float cb = __builtin_amdgcn_fmed3f(b, -kFp8Max<T>, kFp8Max<T>);
+  if constexpr (T == E5MA_E5M2) return (uint32_t)__builtin_amdgcn_cvt_pk_bf8_f32(ca, cb, (int)old, HI);
+  else return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(ca, cb, (int)old, HI);
 }
-__device__ __forceinline__ uint32_t f32_to_e5m2(float x) { return f32_to_fp8<2, 15, 0x47600000u, 0x7Bu>(x); }
-__device__ __forceinline__ uint32_t f32_to_e4m3(float x) { return f32_to_fp8<3, 7, 0x43E00000u, 0x7Eu>(x); }
+// four codes, v0 in byte 0 .. v3 in byte 3
+template <int T> __device__ __forceinline__ uint32_t f32x4_to_fp8(float v0, float v1, float v2, float v3) {
+  uint32_t r = fp8_pair_into<T, true>(v2, v3, fp8_pair_into<T, false>(v0, v1, 0u));
+  if (v0 != v0) r = (r & 0xFFFFFF00u) | 0x0000007Fu;
+  if (v1 != v1) r = (r & 0xFFFF00FFu) | 0x00007F00u;
+  if (v2 != v2) r = (r & 0xFF00FFFFu) | 0x007F0000u;
+  if (v3 != v3) r = (r & 0x00FFFFFFu) | 0x7F000000u;
+  return r;
+}
+template <int T> __device__ __forceinline__ uint32_t f32_to_fp8_code(float x) {
+  return x != x ? 0x7Fu : fp8_pair_into<T, false>(x, x, 0u) & 0xFFu;
+}
+__device__ __forceinline__ uint32_t f32_to_e5m2(float x) { return f32_to_fp8_code<E5MA_E5M2>(x); }
+__device__ __forceinline__ uint32_t f32_to_e4m3(float x) { return f32_to_fp8_code<E5MA_E4M3>(x); }
 template <int T> __device__ __forceinline__ uint32_t f32_to_fp8t(float x) {
   return T == E5MA_E5M2 ? f32_to_e5m2(x) : f32_to_e4m3(x);
 }
@@ -128,8 +137,7 @@ template <int T> __device__ __forceinline__ void store4_t(void *p, size_t i, con
   if constexpr (T == E5MA_FP32) {
     *(float4 *)dp = make_float4(v[0], v[1], v[2], v[3]);
   } else if constexpr (is_fp8(T)) {
-    *(uint32_t *)dp = encode_t<T>(v[0], qscale) | encode_t<T>(v[1], qscale) << 8 | encode_t<T>(v[2], qscale) << 16 |
-                      encode_t<T>(v[3], qscale) << 24;
+    *(uint32_t *)dp = f32x4_to_fp8<T>(v[0] * qscale, v[1] * qscale, v[2] * qscale, v[3] * qscale);
   } else {
     *(uint2 *)dp = make_uint2(encode_t<T>(v[0], qscale) | encode_t<T>(v[1], qscale) << 16,
                               encode_t<T>(v[2], qscale) | encode_t<T>(v[3], qscale) << 16);

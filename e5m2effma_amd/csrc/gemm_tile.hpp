@@ -267,8 +267,7 @@ __device__ __forceinline__ float general_half(const Epilogue &e, const EpiState 
         if constexpr (DT == E5MA_FP32) {
           *(float4 *)dp = make_float4(v[0], v[1], v[2], v[3]);
         } else if constexpr (is_fp8(DT)) {
-          *(uint32_t *)dp = encode_t<DT>(v[0], st.qscale) | encode_t<DT>(v[1], st.qscale) << 8 |
-                            encode_t<DT>(v[2], st.qscale) << 16 | encode_t<DT>(v[3], st.qscale) << 24;
+          *(uint32_t *)dp = f32x4_to_fp8<DT>(v[0] * st.qscale, v[1] * st.qscale, v[2] * st.qscale, v[3] * st.qscale);
         } else {
           *(uint2 *)dp = make_uint2(encode_t<DT>(v[0], 1.f) | encode_t<DT>(v[1], 1.f) << 16,
                                     encode_t<DT>(v[2], 1.f) | encode_t<DT>(v[3], 1.f) << 16);
@@ -561,9 +560,7 @@ __device__ __forceinline__ float staged_general(const Epilogue &e, v16f (&acc)[4
         if constexpr (DT == E5MA_FP32) {
           __builtin_nontemporal_store(v4f{v[0], v[1], v[2], v[3]}, (v4f *)dp);
         } else if constexpr (is_fp8(DT)) {
-          __builtin_nontemporal_store(encode_t<DT>(v[0], qs) | encode_t<DT>(v[1], qs) << 8 |
-                                          encode_t<DT>(v[2], qs) << 16 | encode_t<DT>(v[3], qs) << 24,
-                                      (uint32_t *)dp);
+          __builtin_nontemporal_store(f32x4_to_fp8<DT>(v[0] * qs, v[1] * qs, v[2] * qs, v[3] * qs), (uint32_t *)dp);
         } else {
           __builtin_nontemporal_store(v2u{encode_t<DT>(v[0], 1.f) | encode_t<DT>(v[1], 1.f) << 16,
                                           encode_t<DT>(v[2], 1.f) | encode_t<DT>(v[3], 1.f) << 16},

@@ -95,9 +95,10 @@ __global__ __launch_bounds__(kThreads) void q_cast_kernel(const void *__restrict
       Pack<TI, kVec> in;
       in.load(src, c * kVec);
       Pack<TO, kVec, E5MA_QUANT_NT_OUT> out;
-      out.clear();
+      float v[kVec];
 #pragma unroll
-      for (int e = 0; e < kVec; ++e) out.put(e, in.get(e, sinv), qs);
+      for (int e = 0; e < kVec; ++e) v[e] = in.get(e, sinv);
+      out.set(v, qs);
       out.store(dst, c * kVec);
     }
     tail = nvec * kVec;
@@ -143,9 +144,10 @@ __global__ __launch_bounds__(kThreads) void q_rows_kernel(const void *__restrict
       Pack<TI, kVec> in;
       in.load(src, base + c * kVec);
       Pack<TO, kVec, E5MA_QUANT_NT_OUT> out;
-      out.clear();
+      float v[kVec];
 #pragma unroll
-      for (int e = 0; e < kVec; ++e) out.put(e, in.get(e, sinv), qs);
+      for (int e = 0; e < kVec; ++e) v[e] = in.get(e, sinv);
+      out.set(v, qs);
       out.store(dst, base + c * kVec);
     }
   }
@@ -192,9 +194,10 @@ __global__ __launch_bounds__(kThreads) void q_rows_blk_kernel(const void *__rest
   for (int q = 0; q < CPL; ++q)
     if (t + kThreads * q < nvec) {
       Pack<TO, kVec, E5MA_QUANT_NT_OUT> out;
-      out.clear();
+      float v[kVec];
 #pragma unroll
-      for (int e = 0; e < kVec; ++e) out.put(e, in[q].get(e, sinv), qs);
+      for (int e = 0; e < kVec; ++e) v[e] = in[q].get(e, sinv);
+      out.set(v, qs);
       out.store(dst, base + (size_t)(t + kThreads * q) * kVec);
     }
   if (t == 0) {

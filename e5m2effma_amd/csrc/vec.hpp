@@ -61,6 +61,18 @@ template <int T, int N, bool NT = false> struct Pack {
 #pragma unroll
     for (int q = 0; q < kWords; ++q) w[q] = 0;
   }
+  // every element from v (FP8: four codes per conversion pair of instructions)
+  __device__ __forceinline__ void set(const float (&v)[N], float qscale) {
+    if constexpr (is_fp8(T) && N % 4 == 0) {
+#pragma unroll
+      for (int q = 0; q < N / 4; ++q)
+        w[q] = f32x4_to_fp8<T>(v[4 * q] * qscale, v[4 * q + 1] * qscale, v[4 * q + 2] * qscale, v[4 * q + 3] * qscale);
+    } else {
+      clear();
+#pragma unroll
+      for (int e = 0; e < N; ++e) put(e, v[e], qscale);
+    }
+  }
   // set element e (freshly cleared pack) to the code of v
   __device__ __forceinline__ void put(int e, float v, float qscale) {
     const uint32_t c = encode_t<T>(v, qscale);
