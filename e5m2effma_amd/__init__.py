@@ -24,6 +24,7 @@ torch's current stream.  Errors: ``TypeError`` (dtype), ``ValueError`` (device, 
 argument), ``NotImplementedError`` (a device other than gfx950), ``RuntimeError`` (runtime failure).
 """
 import ctypes
+import os
 from typing import Optional
 
 import torch
@@ -37,7 +38,7 @@ e4m3 = torch.float8_e4m3fn
 if not hasattr(torch, "e5m2effma"):
     torch.e5m2effma = e5m2
 __all__ = ["matmul", "linear", "cast", "quantize", "adam_step", "AdamW", "Float8Tensor", "quantize_linear_", "gemm_raw", "e5m2",
-           "e4m3", "__version__"]
+           "e4m3", "torch_ops_enabled", "get_include", "__version__"]
 
 _CODE = {torch.float8_e4m3fn: E4M3, torch.bfloat16: BF16, torch.float16: FP16, torch.float32: FP32,
          torch.float8_e5m2: E5M2}
@@ -355,6 +356,23 @@ def adam_step(param: torch.Tensor, grad: torch.Tensor, exp_avg: torch.Tensor, ex
         s = _lib.lib().e5ma_adam(ctypes.byref(cfg), n, ctypes.byref(P), ctypes.byref(G), ctypes.byref(Mo),
                                  ctypes.byref(V), _lib.ref(Q), _stream())
     _check_status(s, "e5ma_adam")
+
+
+def get_include() -> list:
+    """Directories for HIP code that builds on this library (reference ``__init__.py:49-55``): the C ABI
+    headers (``e5m2effma.h``, ``e5m2effma_ext.h``) and the device-side codecs ``e5ma_device.hpp`` (FP8 decode,
+    RNE / saturating encode, typed loads and stores; gfx950 only).  Compile with ``-I`` on both; code built
+    from them is consistent with this version of the library only."""
+    here = os.path.dirname(os.path.abspath(__file__))
+    return [os.path.join(os.path.dirname(here), "include"), os.path.join(here, "csrc")]
+
+
+def torch_ops_enabled() -> bool:
+    """Whether ``torch._scaled_mm`` runs on this library in this process: never.  The reference overrides
+    ``aten::_scaled_mm`` only on GPUs without native FP8 and keeps PyTorch's kernel elsewhere (reference
+    ``__init__.py:165-170``); gfx950 has native FP8 in PyTorch's own ``_scaled_mm``, so nothing is
+    overridden here."""
+    return False
 
 
 def gemm_raw(transa, transb, m, n, k, alpha, A, lda, B, ldb, beta, C, ldc, D, ldd, bias=None, stream=None):

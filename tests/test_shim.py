@@ -15,8 +15,19 @@ def codes_4x16(fmt=F8):
 
 def test_dtype_alias_and_exports():
     assert torch.e5m2effma is torch.float8_e5m2 and fx.e5m2 is torch.float8_e5m2 and fx.e4m3 is torch.float8_e4m3fn
-    for name in ("matmul", "linear", "cast", "quantize", "adam_step", "AdamW", "Float8Tensor", "quantize_linear_"):
+    for name in ("matmul", "linear", "cast", "quantize", "adam_step", "AdamW", "Float8Tensor", "quantize_linear_",
+                 "torch_ops_enabled", "get_include", "__version__"):
         assert name in fx.__all__ and hasattr(fx, name)
+
+
+def test_get_include_and_torch_ops():
+    """get_include() names the directories of the C ABI headers and the device codecs; aten::_scaled_mm is
+    never overridden (gfx950 has native FP8 in PyTorch's own kernel)."""
+    import os
+    inc = fx.get_include()
+    assert os.path.isfile(os.path.join(inc[0], "e5m2effma.h")) and os.path.isfile(os.path.join(inc[0], "e5m2effma_ext.h"))
+    assert os.path.isfile(os.path.join(inc[1], "e5ma_device.hpp"))
+    assert fx.torch_ops_enabled() is False
 
 
 @pytest.mark.parametrize("args,exc,text", [
