@@ -310,8 +310,10 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_f8_kernel(TileArgs t0, Epilo
   for (int blk = blockIdx.x; blk < t0.count; blk += gridDim.x) {
     // lane and thread ids made opaque per tile, so that nothing derived from them is hoisted out of the tile
     // loop and kept live across the K loop (that spilled 184 bytes)
-    int lane = lane0, tid = tid0;
-    asm volatile("" : "+v"(lane), "+v"(tid));
+    // (the wave index too: an LDS address derived from it was otherwise kept in a register across the tile
+    // loop and spilled; without the spill no instance uses scratch memory, at the same speed)
+    int lane = lane0, tid = tid0, wv = wave;
+    asm volatile("" : "+v"(lane), "+v"(tid), "+s"(wv));
     TileArgs t = t0;
     Epilogue e = e0;
     int tm, tn, sp;
@@ -321,7 +323,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_f8_kernel(TileArgs t0, Epilo
 
     v16f acc[4][4];          // started by the K loop's first unit
     v8i a[2][4], b[2][4];  // fragments, double-buffered by unit parity
-    const Loads<PAIR> L = make_loads<AKC, BKC, PAIR>(t, i0, j0, wave, lane);
+    const Loads<PAIR> L = make_loads<AKC, BKC, PAIR>(t, i0, j0, wv, lane);
     k_loop<AT, BT, AKC, BKC, 4>(L, t.k / kUnitK, lane, wm, wn, a, b, acc);
 
     mx = fmaxf(mx, tile_epilogue<EPI>(t, e, acc, i0, j0, wm, wn, lane, tid, simple, vec, sa1, sb1));

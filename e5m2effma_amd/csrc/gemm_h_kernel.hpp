@@ -202,8 +202,8 @@ template <int AT, int BT, bool AKC, bool BKC, int EPI>
 __global__ __launch_bounds__(kThreads, 1) void gemm_h_kernel(TileArgs t0, Epilogue e0, int simple, int vec) {
   using C = Cfg<AT, BT, AKC, BKC>;
   __shared__ float red[kThreads / 64];
-  const int tid0 = threadIdx.x, lane0 = tid0 & 63, wave = __builtin_amdgcn_readfirstlane(tid0 >> 6);
-  const int wm = wave >> 1, wn = wave & 1;
+  const int tid0 = threadIdx.x, lane0 = tid0 & 63, wave0 = __builtin_amdgcn_readfirstlane(tid0 >> 6);
+  const int wm = wave0 >> 1, wn = wave0 & 1;
   float sa1, sb1;  // per-tensor scales: the same for every tile and split
   epilogue_scales(e0, sa1, sb1);
   float mx = 0.f;
@@ -211,8 +211,10 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_h_kernel(TileArgs t0, Epilog
   late_start(t0, 256ull * (t0.k / 16));
   for (int blk = blockIdx.x; blk < t0.count; blk += gridDim.x) {
     // lane and thread ids made opaque per tile, so that nothing derived from them is hoisted out of the tile loop
-    int lane = lane0, tid = tid0;
-    asm volatile("" : "+v"(lane), "+v"(tid));
+    // (the wave index too: values derived from it were otherwise kept in registers across the tile loop and
+    // spilled, 32 registers in the full-tile write-out's instances; none uses scratch memory now)
+    int lane = lane0, tid = tid0, wave = wave0;
+    asm volatile("" : "+v"(lane), "+v"(tid), "+s"(wave));
     TileArgs t = t0;
     Epilogue e = e0;
     int tm, tn, sp;

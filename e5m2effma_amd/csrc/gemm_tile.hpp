@@ -72,13 +72,16 @@ struct TileArgs {
 // works on one split (one K slice of the operands in its L2); then tiles are grouped kGroupM m-tiles
 // at a time.
 __device__ __forceinline__ void tile_of(int b, const TileArgs &t, int &tm, int &tn, int &split) {
-  const int tiles = t.tiles_m * t.tiles_n, total = t.count;
+  int tiles = t.tiles_m * t.tiles_n, per_group = kGroupM * t.tiles_n;
+  // opaque per call: a persistent kernel then divides afresh per tile instead of keeping the divisions'
+  // reciprocals live across its tile loop (they were spilled to scratch; the time was the same either way)
+  asm volatile("" : "+s"(tiles), "+s"(per_group));
+  const int total = t.count;
   int x = b;
   if ((total & 7) == 0) x = (b & 7) * (total >> 3) + (b >> 3);
   x += t.first;
   split = x / tiles;
   x -= split * tiles;
-  const int per_group = kGroupM * t.tiles_n;
   const int g = x / per_group, r = x - g * per_group;
   const int gm = min(kGroupM, t.tiles_m - g * kGroupM);
   tm = g * kGroupM + r % gm;
