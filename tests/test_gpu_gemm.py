@@ -222,24 +222,28 @@ def test_f8_fast_layouts_fp8_output(dev, ta, tb):
     assert bad == 0, first
 
 
-@pytest.mark.parametrize("ta,tb,adt,bdt,ddt,k", [(1, 0, E5, E4, E5, 8192), (0, 0, E4, E5, E4, 8192),
-                                                 (0, 1, E5, E5, E5, 8192), (1, 1, E4, E4, E4, 8192),
-                                                 (1, 0, E4, B16, E5, 1024), (0, 1, E5, E4, E4, 1024)])
-def test_fp8_output_staged_as_codes(dev, ta, tb, adt, bdt, ddt, k):
+@pytest.mark.parametrize("ta,tb,adt,bdt,ddt,k,m,n", [(1, 0, E5, E4, E5, 8192, 528, 304),
+                                                     (0, 0, E4, E5, E4, 8192, 528, 304),
+                                                     (0, 1, E5, E5, E5, 8192, 528, 304),
+                                                     (1, 1, E4, E4, E4, 8192, 528, 304),
+                                                     (1, 0, E4, B16, E5, 1024, 528, 304),
+                                                     (0, 1, E5, E4, E4, 1024, 528, 304),
+                                                     (1, 0, E5, E5, E5, 8192, 16, 16),
+                                                     (1, 1, E5, E4, E4, 8192, 768, 512)])
+def test_fp8_output_staged_as_codes(dev, ta, tb, adt, bdt, ddt, k, m, n):
     """FP8 D with 16-byte aligned columns (ldd % 16 == 0, m % 16 == 0), no bias, beta = 0: the write-out that
     stages the tile as FP8 codes, on both matrix-core kernels.  m = 528, n = 304 give full tiles and edge
-    tiles in both directions (16 rows, 48 columns); row-wise sa and column-wise sb (per tensor for a BF16 B),
-    scale and amax; Inf / NaN codes in A make saturated and NaN outputs.  The padding rows of D (ldd = m + 16)
-    must stay untouched."""
-    rng = np.random.default_rng(ta * 2 + tb + 16 * ddt + k)
-    m, n = 528, 304
+    tiles in both directions (16 rows, 48 columns); 16 x 16 is a single edge tile; 768 x 512 full tiles only.
+    Row-wise sa and column-wise sb (none for a BF16 B), scale and amax; Inf / NaN codes in A make saturated
+    and NaN outputs.  The padding rows of D (ldd = m + 16) must stay untouched."""
+    rng = np.random.default_rng(ta * 2 + tb + 16 * ddt + k + m)
     sa = rng.uniform(0.25, 2.0, m).astype(np.float32)
     sb = rng.uniform(0.25, 2.0, n).astype(np.float32) if bdt != B16 else None
     case = gu.GemmCase(rng, ta, tb, m, n, k, adt, bdt, ddt=ddt, alpha=0.75, sa=sa, sb=sb, qscale=4.0, amax=True,
                        pad=0, ldd=m + 16, dist="normal", sigma=2.0)
     A = case.A.copy()
     inf, nan = (0x7C, 0x7E) if adt == E5 else (0x7F, 0x7F)  # E4M3 has no Inf: NaN codes only
-    for r, code in ((3, inf), (300, nan), (520, inf | 0x80)):  # row 520 lies in the 16-row edge tile
+    for r, code in ((3, inf), (min(300, m - 2), nan), (m - 8, inf | 0x80)):  # row m - 8: the last 16-row chunk
         A[r * case.lda + 5 if ta else 5 * case.lda + r] = code
     case.A = A
     s, D, amax = case.run(dev)
